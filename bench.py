@@ -1,0 +1,211 @@
+"""Benchmark: AR-aware 3D block-sparse attention forward on one MI355X.
+
+A step is one ``run_sparse_attention`` call of the HY-WorldPlay decode entry
+point on resident bf16 inputs: Q/K/V tile gather + pool, block mask, block-sparse
+attention, untile.  Default workload (``--workload hy``): B=1, 16 heads, D=128,
+30x52 latent, Lq = 4 frames (6240 tokens), Lk = 12 frames (18720 tokens),
+2x8x8 tiles, 30% keep ratio plus the forced diagonal and sink blocks.
+
+Prints one JSON line.  ``value`` is TFLOP/s over the retained blocks for the
+whole call; the attention kernel's own rate, its share of the bf16 MFMA peak,
+a dense GPU comparator (torch SDPA at the same shape) and a CPU baseline (the
+reference's dense-masked torch semantics on the host, on a bounded sample of
+heads) are reported beside it.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "light-interaction-project_amd"))
+sys.path.insert(0, REPO)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="hy")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-heads", type=int, default=4, help="heads timed for the CPU baseline sample")
+    ap.add_argument("--seed", type=int, default=0)
+    return ap.parse_args()
+
+
+def event_loop(fn, iters, stream):
+    """Average ms of ``fn`` over ``iters`` launches, timed with events on ``stream``; also per-call ms list."""
+    import torch
+
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
+    torch.cuda.synchronize()
+    for i in range(iters):
+        starts[i].record(stream)
+        fn()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return sum(per) / len(per), per
+
+
+def pct(xs, p):
+    xs = sorted(xs)
+    return xs[min(len(xs) - 1, max(0, int(round(p / 100.0 * (len(xs) - 1)))))]
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): the sparse-attention path is "
+              "single-GPU; head sharding over several GPUs is a design note, not a measured path.", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from li_sparse import _core, _pipeline
+    from li_sparse.hy.ar_sparse_operation import fast_generate_indices, run_sparse_attention
+    from li_sparse.workloads import WORKLOADS, make_qkv
+
+    wl = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    q, k, v = make_qkv(wl, seed=args.seed, layout="blhd")
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    empty = torch.empty((wl.batch, wl.heads, 0, wl.head_dim), dtype=torch.bfloat16, device=dev)
+    g = _pipeline.geometry(wl.latent_hw, wl.tile, wl.lq, wl.lk, 0)
+    params = wl.sparse_params(g.nq_blk)
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        return run_sparse_attention(qd, empty, empty, kd, vd, 1, wl.latent_hw, params)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = None
+    for _ in range(args.steps):
+        out = step()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    step_ms, per_step = event_loop(step, args.steps, stream)
+
+    # Work actually retained: counts from the emitted block lists.
+    B, H, D, bs = wl.batch, wl.heads, wl.head_dim, g.bs
+    q_t = torch.empty((B, H, g.nq_blk, bs, D), dtype=torch.bfloat16, device=dev)
+    q_p = torch.empty((B, H, g.nq_blk, D), dtype=torch.bfloat16, device=dev)
+    k_all = torch.empty((B, H, g.nk_blk, bs, D), dtype=torch.bfloat16, device=dev)
+    v_all = torch.empty_like(k_all)
+    k_p = torch.empty((B, H, g.nk_blk, D), dtype=torch.bfloat16, device=dev)
+    _core.q_prep(qd, q_t, q_p, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    _core.kv_prep(kd, vd, k_all, v_all, k_p, 0, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    ind, cnt = fast_generate_indices(q_p, k_p, 0, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), params, dev)
+    torch.cuda.synchronize()
+    counts = cnt.cpu().numpy()
+    flops = float(counts.sum()) * 4.0 * bs * bs * D
+    qf, kf, vf = q_t.flatten(2, 3), k_all.flatten(2, 3), v_all.flatten(2, 3)
+    scale = 1.0 / math.sqrt(D)
+    attn = lambda: _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs)  # noqa: E731
+    for _ in range(5):
+        attn()
+    attn_ms, attn_per = event_loop(attn, args.steps, stream)
+    attn_tflops = flops / (attn_ms * 1e-3) / 1e12
+
+    # Dense comparators: torch SDPA (valid tokens) and this kernel with every block kept.
+    sdpa = lambda: torch.nn.functional.scaled_dot_product_attention(qd, kd, vd)  # noqa: E731
+    for _ in range(3):
+        sdpa()
+    dense_ms, _ = event_loop(sdpa, max(5, args.steps // 5), stream)
+    dense_flops = 4.0 * wl.lq * wl.lk * D * H * B
+    all_ind = torch.arange(g.nk_blk, dtype=torch.int32, device=dev).expand(B, H, g.nq_blk, g.nk_blk).contiguous()
+    all_cnt = torch.full((B, H, g.nq_blk), g.nk_blk, dtype=torch.int32, device=dev)
+    full = lambda: _core.bsa_forward(qf, kf, vf, all_ind, all_cnt, scale, bs)  # noqa: E731
+    full()
+    full_ms, _ = event_loop(full, max(5, args.steps // 5), stream)
+    full_flops = float(B * H * g.nq_blk * g.nk_blk) * 4.0 * bs * bs * D
+
+    gather_bytes = 2.0 * (wl.lq + 2 * wl.lk) * H * D * B + 2.0 * (g.nq_blk + 2 * g.nk_blk) * bs * H * D * B
+
+    result = {
+        "metric": "sparse-attn fwd ms/call + TFLOPS (% MFMA peak) at HY shape, 30% keep",
+        "value": round(flops / (step_ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded smooth (t,h,w) field + 0.5*N(0,1), bf16, Q pre-scaled by 1/sqrt(D))",
+        "config": {"workload": wl.note, "batch": B, "heads": H, "head_dim": D, "lq": wl.lq, "lk": wl.lk,
+                   "tile": list(wl.tile), "keep_ratio": wl.ratio, "block_size": bs, "nq_blocks": g.nq_blk,
+                   "nk_blocks": g.nk_blk, "kept_blocks_per_row_mean": round(float(counts.mean()), 2),
+                   "parallelism": "single GPU"},
+        "ms_per_call": {"median": round(pct(per_step, 50), 4), "p10": round(pct(per_step, 10), 4),
+                        "p90": round(pct(per_step, 90), 4), "host_wall": round(wall_ms, 4)},
+        "attention_kernel": {"ms": round(attn_ms, 4), "median_ms": round(pct(attn_per, 50), 4),
+                             "tflops": round(attn_tflops, 2),
+                             "pct_bf16_peak": round(100.0 * attn_tflops / PEAK_BF16_TFLOPS, 2),
+                             "retained_gflop": round(flops / 1e9, 2)},
+        "dense_comparator": {"torch_sdpa_ms": round(dense_ms, 4),
+                             "torch_sdpa_tflops": round(dense_flops / (dense_ms * 1e-3) / 1e12, 2),
+                             "own_kernel_all_blocks_ms": round(full_ms, 4),
+                             "own_kernel_all_blocks_tflops": round(full_flops / (full_ms * 1e-3) / 1e12, 2),
+                             "speedup_call_vs_sdpa": round(dense_ms / step_ms, 3),
+                             "speedup_attention_vs_sdpa": round(dense_ms / attn_ms, 3)},
+        "roofline": {"bound": "mfma", "kernel": "bsa_fwd_kernel<bf16,128,128>",
+                     "achieved": round(attn_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "gather_bytes_per_call": gather_bytes,
+    }
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(wl, q, k, v, counts, ind.cpu().numpy(), g, args.cpu_heads, flops)
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline(wl, q, k, v, counts, ind, g, n_heads, flops):
+    """The reference's dense-masked torch semantics on the host CPU, on a bounded sample of heads."""
+    import numpy as np
+    import torch
+
+    from li_sparse.workloads import WORKLOADS  # noqa: F401
+    from oracle import attention as oatt
+    from oracle import tile as otile
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    H, W = wl.latent_hw
+    n_heads = max(1, min(n_heads, wl.heads))
+    heads = [(0, h) for h in range(n_heads)]
+
+    def tiles(x, frames):
+        b = x.contiguous().view(torch.int16).numpy().view(np.uint16)[:, :n_heads]
+        t = otile.tile_gather(b, frames, H, W, wl.tile)
+        return torch.from_numpy(t.reshape(t.shape[0], t.shape[1], -1, t.shape[-1]).view(np.int16)).view(torch.bfloat16)
+
+    qt, kt, vt = tiles(q, wl.frames_q), tiles(k, wl.frames_k), tiles(v, wl.frames_k)
+    t0 = time.perf_counter()
+    oatt.dense_masked_cpu(qt, kt, vt, ind[:, :n_heads], counts[:, :n_heads], 1.0 / math.sqrt(wl.head_dim), g.bs,
+                          head_list=heads)
+    sec = time.perf_counter() - t0
+    sample_flops = float(counts[:, :n_heads].sum()) * 4.0 * g.bs * g.bs * wl.head_dim
+    ms_full = sec * 1e3 * wl.heads / n_heads
+    return {"value": round(sample_flops / sec / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "ms_per_call_scaled": round(ms_full, 1),
+            "sample": f"{n_heads} of {wl.heads} heads of the same call (torch CPU SDPA, fp32 from bf16, boolean "
+                      f"mask expanded from the kept blocks over the tiled/padded layout), {sec:.1f} s; "
+                      f"ms_per_call_scaled = sample time x {wl.heads}/{n_heads}"}
+
+
+if __name__ == "__main__":
+    main()

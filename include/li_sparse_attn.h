@@ -1,0 +1,162 @@
+/*
+ * li_sparse_attn.h -- C ABI of the MI355X (gfx950) AR-aware 3D block-sparse
+ * attention forward.
+ *
+ * Plain C: pointers, sizes and strides only.  Every buffer is allocated by the
+ * caller (device memory); no entry point allocates device memory, keeps a
+ * pointer after it returns, or synchronises the stream.  Strides are in
+ * elements.  Each entry point validates its arguments on the host and returns
+ * LI_OK or a negative status without touching the GPU when they are invalid;
+ * kernels are enqueued on `stream` (a hipStream_t, NULL = default stream).
+ *
+ * Element types: LI_DTYPE_BF16 (default) or LI_DTYPE_F16 for Q/K/V, tiles,
+ * pools and outputs.  Index lists are int32.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   HYAR = hy-worldplay/files/hyvideo/models/transformers/modules/ar_sparse_operation.py
+ *   HYKV = hy-worldplay/files/hyvideo/models/transformers/modules/bi_sparse_operation_for_KV_cache.py
+ *   HYK  = hy-worldplay/files/hyvideo/models/transformers/modules/longcat_kernel.py
+ *   MGS  = matrix-game-3.0/files/wan/modules/bi_sparse_operation.py
+ */
+#ifndef LI_SPARSE_ATTN_H
+#define LI_SPARSE_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum li_status {
+  LI_OK = 0,
+  LI_ERR_INVALID_ARG = -1,   /* null pointer, negative or zero size */
+  LI_ERR_SHAPE = -2,         /* inconsistent shapes / geometry */
+  LI_ERR_K_LEN = -3,         /* K length not a multiple of the logical block size (HYK:192-193) */
+  LI_ERR_INDEX_RANGE = -4,   /* block index out of range (HYK:194-195) */
+  LI_ERR_UNSUPPORTED = -5,   /* head_dim / block size / dtype not built */
+  LI_ERR_LAUNCH = -6,        /* HIP launch error */
+  LI_ERR_TOO_LARGE = -7      /* key-block count above the mask builder's limit */
+};
+
+enum li_dtype { LI_DTYPE_BF16 = 0, LI_DTYPE_F16 = 1 };
+
+/* Latent grid and tile: frames T, height H, width W; tile (tt, th, tw);
+ * nh = ceil(H/th), nw = ceil(W/tw) tiles per t-slab (HYAR:322). */
+typedef struct li_tile_geom {
+  int32_t T, H, W;
+  int32_t tt, th, tw;
+  int32_t nh, nw;
+} li_tile_geom;
+
+/* ABI version (bumped on any signature change). */
+int li_abi_version(void);
+/* Static text for a status code. */
+const char* li_status_string(int status);
+
+/*
+ * Q tile gather + mean pool.  Replaces launch_q_prep(src, dst, mean, T, H, W,
+ * tt, th, tw, nh, nw) and _fused_q_prep_kernel (HYAR:26-70, 166-181; HYKV:27-73,
+ * 168-181; MGS:25-64, 142-152).
+ *   src  (B, NH, L, D), any strides, L >= T*H*W
+ *   dst  (B, NH, nblk, BS, D) tiles, any strides (nblk = ceil(T/tt)*nh*nw, BS = tt*th*tw)
+ *   mean (B, NH, nblk, D) pooled means: bf16/f16( fp32 sum over BS rows / BS ), padding included
+ * Rows outside the (T, H, W) grid are written as zeros.
+ */
+int li_q_prep(int dtype, int32_t B, int32_t NH, int32_t D,
+              const void* src, const int64_t src_strides[4],
+              void* dst, const int64_t dst_strides[5],
+              void* mean, const int64_t mean_strides[4],
+              const li_tile_geom* geom, void* stream);
+
+/*
+ * K/V tile gather + K mean pool.  Replaces launch_kv_prep(k_src, v_src, k_dst,
+ * v_dst, k_mean, dst_off, pool_off, T, H, W, tt, th, tw, nh, nw) and
+ * _fused_kv_prep_kernel (HYAR:75-122, 183-202; HYKV:78-126; MGS:66-107, 154-166).
+ * Tiles are written at block (blk + dst_off), pools at (blk + pool_off).
+ */
+int li_kv_prep(int dtype, int32_t B, int32_t NH, int32_t D,
+               const void* k_src, const int64_t k_src_strides[4],
+               const void* v_src, const int64_t v_src_strides[4],
+               void* k_dst, const int64_t k_dst_strides[5],
+               void* v_dst, const int64_t v_dst_strides[5],
+               void* k_mean, const int64_t mean_strides[4],
+               int64_t dst_off, int64_t pool_off,
+               const li_tile_geom* geom, void* stream);
+
+/*
+ * Untile scatter.  Replaces launch_untile(src, dst, T, H, W, tt, th, tw, nh, nw)
+ * and _fused_untile_kernel (HYAR:127-161, 204-218; MGS:109-140, 168-177).
+ *   src (B, NH, nblk, BS, D) tiles, any strides; dst (B, NH, L, D), any strides.
+ * Only slots inside the (T, H, W) grid are stored (padding dropped).
+ */
+int li_untile(int dtype, int32_t B, int32_t NH, int32_t D,
+              const void* src, const int64_t src_strides[5],
+              void* dst, const int64_t dst_strides[4],
+              const li_tile_geom* geom, void* stream);
+
+/* Similarity metric of the block-mask builder (HYAR:250-256). */
+enum li_metric { LI_METRIC_COSINE = 0, LI_METRIC_SCALED_DOT = 1, LI_METRIC_DOT = 2 };
+/* Budget rule: HISTORY = nf + int((nk - nf) * ratio), clamped to [1, nk] (HYAR:268-272);
+ * TOTAL = min(max(int(nk * ratio), min_budget), nk) (HYKV:282-285). */
+enum li_budget_mode { LI_BUDGET_HISTORY = 0, LI_BUDGET_TOTAL = 1 };
+
+typedef struct li_mask_params {
+  int32_t metric;           /* li_metric */
+  int32_t budget_mode;      /* li_budget_mode */
+  double topk_ratio;        /* Python float semantics: int() truncation of a double product */
+  int32_t min_budget;       /* TOTAL mode floor (7 in the reference) */
+  int32_t n_recent;         /* trailing key blocks always kept (recent_protect slabs) */
+  int32_t force_diag;       /* keep the key block at the query's key-grid position */
+  int32_t force_sink;       /* keep the t-slab-0 key block at the query's (h, w) */
+  int32_t force_neighbors;  /* keep key blocks at 3D Manhattan distance <= 1 (HYKV:268-280) */
+  int32_t nq, nk;           /* query / key visual block counts */
+  int32_t nh, nw;           /* tiles per slab (key grid) */
+  int32_t num_txt_blk;      /* text blocks prepended to every row (HYAR:277-281) */
+  int32_t kmax;             /* row length of `indices` (>= num_txt_blk + largest budget) */
+  const int32_t* row_budget;/* optional device (nq,) per-row visual totals (ragged rows); NULL = rule */
+  float scale;              /* 1/sqrt(D) for LI_METRIC_SCALED_DOT, as fp32 */
+} li_mask_params;
+
+/*
+ * Block-mask builder.  Replaces fast_generate_indices (HYAR:223-284) and
+ * generate_prefill_indices (HYKV:220-296; MGS:179-234).
+ *   q_pool (B, NH, nq, D), k_pool (B, NH, nk, D): pooled means, any strides
+ *   indices (B, NH, nq, kmax) int32 contiguous: text blocks, then the selected
+ *     visual blocks ascending (+num_txt_blk); unused tail entries are 0
+ *   counts (B, NH, nq) int32 contiguous
+ *   scores (B, NH, nq, nk) optional (NULL): the bf16/f16 similarity scores
+ * Selection: every forced block, then the top (k - n_forced) non-forced blocks by
+ * score, ties to the lower block index.  nk <= 12288.
+ */
+int li_block_mask(int dtype, int32_t B, int32_t NH, int32_t D,
+                  const void* q_pool, const int64_t q_pool_strides[4],
+                  const void* k_pool, const int64_t k_pool_strides[4],
+                  const li_mask_params* params,
+                  int32_t* indices, int32_t* counts, void* scores, void* stream);
+
+/*
+ * Block-sparse flash-attention forward.  Replaces longcat_flash_attn(q, k, v,
+ * block_indices, block_counts, sm_scale, logical_block_size) and
+ * _attn_fwd_bsa_align (HYK:27-155, 158-233; MG longcat_kernel.py:28-134, 137-190).
+ *   q (B, NH, Lq, D), k / v (B, NH, Lk, D): contiguous; Lk % block_size == 0
+ *   block_indices (B, NH, ceil(Lq/block_size), n_cols) int32, any strides
+ *   block_counts (B, NH, ceil(Lq/block_size)) int32, any strides
+ *   out (B, NH, Lq, D) contiguous; lse (B, NH, Lq) fp32 log2-domain LSE or NULL
+ * Query tile m (block_size rows) attends to key blocks
+ * block_indices[b,h,m,:block_counts[b,h,m]] (each block_size rows of K/V).
+ * Zero rows inside kept blocks take part in the softmax, as in the reference.
+ * Out-of-range ids are skipped on the device (callers validate beforehand).
+ * Built for block_size in {64, 128} and D in {64, 128}.
+ */
+int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int32_t D,
+               const void* q, const void* k, const void* v,
+               const int32_t* block_indices, const int64_t idx_strides[4], int32_t n_cols,
+               const int32_t* block_counts, const int64_t cnt_strides[3],
+               float sm_scale, int32_t block_size,
+               void* out, float* lse, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LI_SPARSE_ATTN_H */

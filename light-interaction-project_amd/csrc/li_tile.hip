@@ -1,0 +1,290 @@
+// 3D (t,h,w) tile gather with fixed-order fp32 mean pooling, and its inverse
+// scatter, for gfx950.
+//
+// Replaces the Triton kernels _fused_q_prep_kernel, _fused_kv_prep_kernel and
+// _fused_untile_kernel (hy-worldplay/.../ar_sparse_operation.py:26-161; copies in
+// bi_sparse_operation_for_KV_cache.py:27-163 and matrix-game-3.0/.../bi_sparse_operation.py:25-140).
+//
+// Index maps (ar_sparse_operation.py:42-59): block blk -> (ct, ch, cw) =
+// (blk / (nh*nw), (blk / nw) % nh, blk % nw); tile row f -> (ft, fh, fw) =
+// (f / (tw*th), (f / tw) % th, f % tw); token l = t*H*W + h*W + w.
+//
+// One 256-thread workgroup per (tile, batch*head).  Thread t owns the 16-byte
+// column chunk c = t % (D/8) (8 elements) of tile rows f = g, g+NG, ... with
+// g = t / (D/8) and NG = 256 / (D/8): sixteen consecutive threads move one
+// 256-byte token row, so every global access is a coalesced 16-byte vector
+// access whenever the row is contiguous.  The pool sums each group's rows
+// sequentially in fp32 from +0.0, then combines the NG partials with the
+// pairwise tree s[g] += s[g + stride], stride = NG/2 .. 1, and divides by BS.
+// That order is fixed so the pooled values are reproducible bit for bit.
+#include "li_common.hpp"
+
+namespace li {
+namespace {
+
+struct GatherArgs {
+  const uint16_t* src[2];
+  int64_t ss[2][4];
+  uint16_t* dst[2];
+  int64_t ds[2][5];
+  uint16_t* mean;
+  int64_t ms[4];
+  int64_t dst_off, pool_off;
+  int32_t NH, bs;
+  li_tile_geom g;
+  int32_t vec_src, vec_dst;
+};
+
+__device__ __forceinline__ u32x4 load8(const uint16_t* p, int64_t stride, bool vec) {
+  if (vec) return *reinterpret_cast<const u32x4*>(p);
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = pack2(p[(2 * i) * stride], p[(2 * i + 1) * stride]);
+  return r;
+}
+
+__device__ __forceinline__ void store8(uint16_t* p, int64_t stride, bool vec, u32x4 v) {
+  if (vec) {
+    *reinterpret_cast<u32x4*>(p) = v;
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    p[(2 * i) * stride] = uint16_t(v[i] & 0xFFFFu);
+    p[(2 * i + 1) * stride] = uint16_t(v[i] >> 16);
+  }
+}
+
+template <typename E, int D, int NT>
+__global__ __launch_bounds__(256) void gather_pool_kernel(GatherArgs a) {
+  constexpr int CPR = D / 8;
+  constexpr int NG = 256 / CPR;
+  __shared__ float red[NG][D];
+
+  const int blk = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / a.NH, h = bh % a.NH;
+  const int tid = threadIdx.x;
+  const int c = tid % CPR, g0 = tid / CPR;
+  const li_tile_geom& g = a.g;
+  const int cw = blk % g.nw, rem = blk / g.nw;
+  const int ch = rem % g.nh, ct = rem / g.nh;
+  const bool vs = a.vec_src != 0, vd = a.vec_dst != 0;
+
+  const uint16_t* sbase[NT];
+  uint16_t* dbase[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    sbase[n] = a.src[n] + b * a.ss[n][0] + h * a.ss[n][1] + (int64_t)(8 * c) * a.ss[n][3];
+    dbase[n] = a.dst[n] + b * a.ds[n][0] + h * a.ds[n][1] + (blk + a.dst_off) * a.ds[n][2] +
+               (int64_t)(8 * c) * a.ds[n][4];
+  }
+
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+
+  for (int f = g0; f < a.bs; f += NG) {
+    const int fw = f % g.tw, r = f / g.tw;
+    const int fh = r % g.th, ft = r / g.th;
+    const int t = ct * g.tt + ft, hh = ch * g.th + fh, w = cw * g.tw + fw;
+    const bool valid = (t < g.T) && (hh < g.H) && (w < g.W);
+    const int64_t l = (int64_t)t * g.H * g.W + (int64_t)hh * g.W + w;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (valid) v = load8(sbase[n] + l * a.ss[n][2], a.ss[n][3], vs);
+      store8(dbase[n] + (int64_t)f * a.ds[n][3], a.ds[n][4], vd, v);
+      if (n == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[2 * i] = acc[2 * i] + E::to_f32(uint16_t(v[i] & 0xFFFFu));
+          acc[2 * i + 1] = acc[2 * i + 1] + E::to_f32(uint16_t(v[i] >> 16));
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < 8; ++i) red[g0][8 * c + i] = acc[i];
+  __syncthreads();
+  if (tid < D) {
+    float s[NG];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) s[i] = red[i][tid];
+#pragma unroll
+    for (int stride = NG / 2; stride >= 1; stride /= 2) {
+#pragma unroll
+      for (int i = 0; i < stride; ++i) s[i] = s[i] + s[i + stride];
+    }
+    const float mean = s[0] / (float)a.bs;
+    a.mean[b * a.ms[0] + h * a.ms[1] + (blk + a.pool_off) * a.ms[2] + (int64_t)tid * a.ms[3]] = E::from_f32(mean);
+  }
+}
+
+struct UntileArgs {
+  const uint16_t* src;
+  int64_t ss[5];
+  uint16_t* dst;
+  int64_t ds[4];
+  int32_t NH, bs;
+  li_tile_geom g;
+  int32_t vec_src, vec_dst;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void untile_kernel(UntileArgs a) {
+  constexpr int CPR = D / 8;
+  constexpr int NG = 256 / CPR;
+  const int blk = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / a.NH, h = bh % a.NH;
+  const int tid = threadIdx.x;
+  const int c = tid % CPR, g0 = tid / CPR;
+  const li_tile_geom& g = a.g;
+  const int cw = blk % g.nw, rem = blk / g.nw;
+  const int ch = rem % g.nh, ct = rem / g.nh;
+  const bool vs = a.vec_src != 0, vd = a.vec_dst != 0;
+  const uint16_t* sbase = a.src + b * a.ss[0] + h * a.ss[1] + blk * a.ss[2] + (int64_t)(8 * c) * a.ss[4];
+  uint16_t* dbase = a.dst + b * a.ds[0] + h * a.ds[1] + (int64_t)(8 * c) * a.ds[3];
+  for (int f = g0; f < a.bs; f += NG) {
+    const int fw = f % g.tw, r = f / g.tw;
+    const int fh = r % g.th, ft = r / g.th;
+    const int t = ct * g.tt + ft, hh = ch * g.th + fh, w = cw * g.tw + fw;
+    if ((t < g.T) && (hh < g.H) && (w < g.W)) {
+      const int64_t l = (int64_t)t * g.H * g.W + (int64_t)hh * g.W + w;
+      u32x4 v = load8(sbase + (int64_t)f * a.ss[3], a.ss[4], vs);
+      store8(dbase + l * a.ds[2], a.ds[3], vd, v);
+    }
+  }
+}
+
+// 16-byte vector access is legal when the innermost stride is 1 and every row
+// start (and the base pointer) is 16-byte aligned.
+bool vec_ok(const void* p, const int64_t* strides, int nd) {
+  if (strides[nd - 1] != 1) return false;
+  if ((reinterpret_cast<uintptr_t>(p) & 15u) != 0) return false;
+  for (int i = 0; i < nd - 1; ++i)
+    if (strides[i] % 8 != 0) return false;
+  return true;
+}
+
+int check_geom(const li_tile_geom* g) {
+  if (!g) return LI_ERR_INVALID_ARG;
+  if (g->T < 0 || g->H <= 0 || g->W <= 0 || g->tt <= 0 || g->th <= 0 || g->tw <= 0) return LI_ERR_SHAPE;
+  if (g->nh != (g->H + g->th - 1) / g->th || g->nw != (g->W + g->tw - 1) / g->tw) return LI_ERR_SHAPE;
+  return LI_OK;
+}
+
+int64_t num_blocks(const li_tile_geom* g) { return (int64_t)((g->T + g->tt - 1) / g->tt) * g->nh * g->nw; }
+
+template <int NT>
+int launch_gather(int dtype, int32_t B, int32_t NH, int32_t D, GatherArgs& a, const li_tile_geom* geom,
+                  hipStream_t stream) {
+  if (B <= 0 || NH <= 0) return LI_ERR_INVALID_ARG;
+  int st = check_geom(geom);
+  if (st != LI_OK) return st;
+  const int64_t nblk = num_blocks(geom);
+  if (nblk == 0) return LI_OK;
+  if (nblk > 0x7FFFFFFF || (int64_t)B * NH > 65535) return LI_ERR_SHAPE;
+  a.NH = NH;
+  a.bs = geom->tt * geom->th * geom->tw;
+  a.g = *geom;
+  dim3 grid((unsigned)nblk, (unsigned)(B * NH));
+  if (dtype == LI_DTYPE_BF16 && D == 128)
+    hipLaunchKernelGGL((gather_pool_kernel<Bf16, 128, NT>), grid, dim3(256), 0, stream, a);
+  else if (dtype == LI_DTYPE_BF16 && D == 64)
+    hipLaunchKernelGGL((gather_pool_kernel<Bf16, 64, NT>), grid, dim3(256), 0, stream, a);
+  else if (dtype == LI_DTYPE_F16 && D == 128)
+    hipLaunchKernelGGL((gather_pool_kernel<F16, 128, NT>), grid, dim3(256), 0, stream, a);
+  else if (dtype == LI_DTYPE_F16 && D == 64)
+    hipLaunchKernelGGL((gather_pool_kernel<F16, 64, NT>), grid, dim3(256), 0, stream, a);
+  else
+    return LI_ERR_UNSUPPORTED;
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace li
+
+using namespace li;
+
+extern "C" int li_q_prep(int dtype, int32_t B, int32_t NH, int32_t D, const void* src, const int64_t src_strides[4],
+                         void* dst, const int64_t dst_strides[5], void* mean, const int64_t mean_strides[4],
+                         const li_tile_geom* geom, void* stream) {
+  if (!src || !dst || !mean || !src_strides || !dst_strides || !mean_strides) return LI_ERR_INVALID_ARG;
+  GatherArgs a = {};
+  a.src[0] = static_cast<const uint16_t*>(src);
+  a.dst[0] = static_cast<uint16_t*>(dst);
+  for (int i = 0; i < 4; ++i) a.ss[0][i] = src_strides[i];
+  for (int i = 0; i < 5; ++i) a.ds[0][i] = dst_strides[i];
+  a.mean = static_cast<uint16_t*>(mean);
+  for (int i = 0; i < 4; ++i) a.ms[i] = mean_strides[i];
+  a.dst_off = 0;
+  a.pool_off = 0;
+  a.vec_src = vec_ok(src, src_strides, 4);
+  a.vec_dst = vec_ok(dst, dst_strides, 5);
+  return launch_gather<1>(dtype, B, NH, D, a, geom, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int li_kv_prep(int dtype, int32_t B, int32_t NH, int32_t D, const void* k_src,
+                          const int64_t k_src_strides[4], const void* v_src, const int64_t v_src_strides[4],
+                          void* k_dst, const int64_t k_dst_strides[5], void* v_dst, const int64_t v_dst_strides[5],
+                          void* k_mean, const int64_t mean_strides[4], int64_t dst_off, int64_t pool_off,
+                          const li_tile_geom* geom, void* stream) {
+  if (!k_src || !v_src || !k_dst || !v_dst || !k_mean || !k_src_strides || !v_src_strides || !k_dst_strides ||
+      !v_dst_strides || !mean_strides)
+    return LI_ERR_INVALID_ARG;
+  if (dst_off < 0 || pool_off < 0) return LI_ERR_INVALID_ARG;
+  GatherArgs a = {};
+  a.src[0] = static_cast<const uint16_t*>(k_src);
+  a.src[1] = static_cast<const uint16_t*>(v_src);
+  a.dst[0] = static_cast<uint16_t*>(k_dst);
+  a.dst[1] = static_cast<uint16_t*>(v_dst);
+  for (int i = 0; i < 4; ++i) {
+    a.ss[0][i] = k_src_strides[i];
+    a.ss[1][i] = v_src_strides[i];
+    a.ms[i] = mean_strides[i];
+  }
+  for (int i = 0; i < 5; ++i) {
+    a.ds[0][i] = k_dst_strides[i];
+    a.ds[1][i] = v_dst_strides[i];
+  }
+  a.mean = static_cast<uint16_t*>(k_mean);
+  a.dst_off = dst_off;
+  a.pool_off = pool_off;
+  a.vec_src = vec_ok(k_src, k_src_strides, 4) && vec_ok(v_src, v_src_strides, 4);
+  a.vec_dst = vec_ok(k_dst, k_dst_strides, 5) && vec_ok(v_dst, v_dst_strides, 5);
+  return launch_gather<2>(dtype, B, NH, D, a, geom, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int li_untile(int dtype, int32_t B, int32_t NH, int32_t D, const void* src, const int64_t src_strides[5],
+                         void* dst, const int64_t dst_strides[4], const li_tile_geom* geom, void* stream) {
+  if (!src || !dst || !src_strides || !dst_strides) return LI_ERR_INVALID_ARG;
+  if (B <= 0 || NH <= 0) return LI_ERR_INVALID_ARG;
+  if (dtype != LI_DTYPE_BF16 && dtype != LI_DTYPE_F16) return LI_ERR_UNSUPPORTED;
+  int st = check_geom(geom);
+  if (st != LI_OK) return st;
+  const int64_t nblk = num_blocks(geom);
+  if (nblk == 0) return LI_OK;
+  if (nblk > 0x7FFFFFFF || (int64_t)B * NH > 65535) return LI_ERR_SHAPE;
+  UntileArgs a = {};
+  a.src = static_cast<const uint16_t*>(src);
+  a.dst = static_cast<uint16_t*>(dst);
+  for (int i = 0; i < 5; ++i) a.ss[i] = src_strides[i];
+  for (int i = 0; i < 4; ++i) a.ds[i] = dst_strides[i];
+  a.NH = NH;
+  a.bs = geom->tt * geom->th * geom->tw;
+  a.g = *geom;
+  a.vec_src = vec_ok(src, src_strides, 5);
+  a.vec_dst = vec_ok(dst, dst_strides, 4);
+  dim3 grid((unsigned)nblk, (unsigned)(B * NH));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (D == 128)
+    hipLaunchKernelGGL(untile_kernel<128>, grid, dim3(256), 0, s, a);
+  else if (D == 64)
+    hipLaunchKernelGGL(untile_kernel<64>, grid, dim3(256), 0, s, a);
+  else
+    return LI_ERR_UNSUPPORTED;
+  return launch_status();
+}

@@ -1,0 +1,229 @@
+"""Torch-facing launchers over the C ABI (device memory and streams come from torch).
+
+Every function validates shapes on the host, then enqueues one HIP kernel on
+torch's current stream of the tensors' device.  Nothing here synchronises the
+stream or computes on the CPU.
+"""
+import ctypes
+import math
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import MaskParams, TileGeom, check, i64_array, lib
+
+_DTYPES = {torch.bfloat16: _lib.LI_DTYPE_BF16, torch.float16: _lib.LI_DTYPE_F16}
+METRICS = {"cosine": _lib.LI_METRIC_COSINE, "scaled_dot_product": _lib.LI_METRIC_SCALED_DOT}
+
+
+def dtype_code(t):
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; expected bfloat16 or float16") from None
+
+
+def _device_check(*ts):
+    dev = ts[0].device
+    if dev.type != "cuda":
+        raise ValueError("sparse attention tensors must be on a ROCm (cuda) device")
+    for t in ts[1:]:
+        if t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
+    return dev
+
+
+def _stream(dev):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _same_dtype(*ts):
+    for t in ts[1:]:
+        if t.dtype != ts[0].dtype:
+            raise TypeError(f"dtype mismatch: {ts[0].dtype} vs {t.dtype}")
+
+
+def ceil_div(a, b):
+    return (a + b - 1) // b
+
+
+def num_blocks(T, tt, nh, nw):
+    return ceil_div(T, tt) * nh * nw
+
+
+def q_prep(src, dst, mean, T, H, W, tt, th, tw, nh, nw):
+    """Tile gather + mean pool of one tensor (see li_q_prep)."""
+    dev = _device_check(src, dst, mean)
+    _same_dtype(src, dst, mean)
+    B, NH, L, D = src.shape
+    nblk, bs = num_blocks(T, tt, nh, nw), tt * th * tw
+    if L < T * H * W:
+        raise ValueError(f"source length {L} < T*H*W = {T * H * W}")
+    if dst.shape[:2] != (B, NH) or dst.shape[2] < nblk or dst.shape[3:] != (bs, D):
+        raise ValueError(f"tile buffer shape {tuple(dst.shape)} does not hold {nblk} tiles of ({bs}, {D})")
+    if tuple(mean.shape[:2]) != (B, NH) or mean.shape[2] < nblk or mean.shape[3] != D:
+        raise ValueError(f"pool buffer shape {tuple(mean.shape)} does not hold {nblk} rows of {D}")
+    g = TileGeom(T, H, W, tt, th, tw, nh, nw)
+    st = lib.li_q_prep(dtype_code(src), B, NH, D, src.data_ptr(), i64_array(src.stride()), dst.data_ptr(),
+                       i64_array(dst.stride()), mean.data_ptr(), i64_array(mean.stride()), ctypes.byref(g),
+                       _stream(dev))
+    check("li_q_prep", st)
+
+
+def kv_prep(k_src, v_src, k_dst, v_dst, k_mean, dst_off, pool_off, T, H, W, tt, th, tw, nh, nw):
+    """Tile gather of K and V (at block offset dst_off) + K mean pool (at pool_off) (see li_kv_prep)."""
+    dev = _device_check(k_src, v_src, k_dst, v_dst, k_mean)
+    _same_dtype(k_src, v_src, k_dst, v_dst, k_mean)
+    B, NH, L, D = k_src.shape
+    if tuple(v_src.shape) != tuple(k_src.shape):
+        raise ValueError(f"K/V source shapes differ: {tuple(k_src.shape)} vs {tuple(v_src.shape)}")
+    nblk, bs = num_blocks(T, tt, nh, nw), tt * th * tw
+    if L < T * H * W:
+        raise ValueError(f"source length {L} < T*H*W = {T * H * W}")
+    for name, t in (("k_dst", k_dst), ("v_dst", v_dst)):
+        if t.shape[:2] != (B, NH) or t.shape[2] < nblk + dst_off or t.shape[3:] != (bs, D):
+            raise ValueError(f"{name} shape {tuple(t.shape)} does not hold {nblk}+{dst_off} tiles of ({bs}, {D})")
+    if tuple(k_mean.shape[:2]) != (B, NH) or k_mean.shape[2] < nblk + pool_off or k_mean.shape[3] != D:
+        raise ValueError(f"pool buffer shape {tuple(k_mean.shape)} does not hold {nblk}+{pool_off} rows")
+    g = TileGeom(T, H, W, tt, th, tw, nh, nw)
+    st = lib.li_kv_prep(dtype_code(k_src), B, NH, D, k_src.data_ptr(), i64_array(k_src.stride()),
+                        v_src.data_ptr(), i64_array(v_src.stride()), k_dst.data_ptr(), i64_array(k_dst.stride()),
+                        v_dst.data_ptr(), i64_array(v_dst.stride()), k_mean.data_ptr(), i64_array(k_mean.stride()),
+                        int(dst_off), int(pool_off), ctypes.byref(g), _stream(dev))
+    check("li_kv_prep", st)
+
+
+def untile(src, dst, T, H, W, tt, th, tw, nh, nw):
+    """Inverse scatter of tiles into the linear token layout (see li_untile)."""
+    dev = _device_check(src, dst)
+    _same_dtype(src, dst)
+    B, NH, L, D = dst.shape
+    nblk, bs = num_blocks(T, tt, nh, nw), tt * th * tw
+    if L < T * H * W:
+        raise ValueError(f"destination length {L} < T*H*W = {T * H * W}")
+    if src.shape[:2] != (B, NH) or src.shape[2] < nblk or src.shape[3:] != (bs, D):
+        raise ValueError(f"tile buffer shape {tuple(src.shape)} does not hold {nblk} tiles of ({bs}, {D})")
+    g = TileGeom(T, H, W, tt, th, tw, nh, nw)
+    st = lib.li_untile(dtype_code(src), B, NH, D, src.data_ptr(), i64_array(src.stride()), dst.data_ptr(),
+                       i64_array(dst.stride()), ctypes.byref(g), _stream(dev))
+    check("li_untile", st)
+
+
+# ----------------------------------------------------------------------------
+# Block-mask budgets (host side: the forced set and the budget depend only on
+# the block geometry and the parameters, so the row length is known without
+# reading any device data).
+# ----------------------------------------------------------------------------
+def forced_counts(nq, nk, nh, nw, n_recent=0, diag=False, sink=False, neighbors=False):
+    """Number of forced key blocks for every query row (same rules as the mask kernel)."""
+    qb = np.arange(nq)
+    pos = nk - nq + qb
+    j = np.arange(nk)
+    f = np.zeros((nq, nk), dtype=bool)
+    if n_recent > 0:
+        f[:, j >= nk - n_recent] = True
+    if diag:
+        f |= j[None, :] == pos[:, None]
+    if sink:
+        f |= j[None, :] == (qb % (nh * nw))[:, None]
+    if neighbors:
+        hw = nh * nw
+        ok = (pos >= 0) & (pos < nk)
+        p = np.where(ok, pos, 0)
+        dist = (np.abs(p[:, None] // hw - j[None, :] // hw) + np.abs((p[:, None] % hw) // nw - (j[None, :] % hw) // nw)
+                + np.abs(p[:, None] % nw - j[None, :] % nw))
+        f |= (dist <= 1) & ok[:, None]
+    return f.sum(axis=1)
+
+
+def row_budgets(nf, nk, mode, ratio, min_budget=7, row_budget=None):
+    """Visual blocks kept per row (forced included), the same arithmetic as the mask kernel."""
+    nf = np.asarray(nf, dtype=np.int64)
+    if row_budget is not None:
+        k = np.asarray(row_budget, dtype=np.int64)
+        return np.minimum(np.maximum(k, nf), nk)
+    out = np.empty_like(nf)
+    for i, f in enumerate(nf.tolist()):
+        if mode == _lib.LI_BUDGET_HISTORY:
+            k = f + int((nk - f) * ratio)
+            k = min(max(k, 1 if nk > 0 else 0), nk)
+        else:
+            k = min(max(int(nk * ratio), min_budget), nk)
+        out[i] = max(k, f)
+    return out
+
+
+def block_mask(q_pool, k_pool, *, metric, budget_mode, ratio, nh, nw, num_txt_blk=0, n_recent=0,
+               force_diag=False, force_sink=False, force_neighbors=False, min_budget=7, row_budget=None,
+               return_scores=False):
+    """Block selection on the device (see li_block_mask).
+
+    Returns ``(indices (B,H,nq,kmax) int32, counts (B,H,nq) int32)`` (+ scores if asked), where
+    ``kmax = num_txt_blk + max row budget``.
+    """
+    dev = _device_check(q_pool, k_pool)
+    _same_dtype(q_pool, k_pool)
+    B, NH, nq, D = q_pool.shape
+    nk = k_pool.shape[2]
+    if tuple(k_pool.shape[:2]) != (B, NH) or k_pool.shape[3] != D:
+        raise ValueError(f"pool shapes differ: {tuple(q_pool.shape)} vs {tuple(k_pool.shape)}")
+    metric_code = METRICS.get(metric, _lib.LI_METRIC_DOT)
+    nf = forced_counts(nq, nk, nh, nw, n_recent, force_diag, force_sink, force_neighbors)
+    rb_dev = None
+    if row_budget is not None:
+        rb = np.asarray(row_budget, dtype=np.int64).reshape(-1)
+        if rb.size != nq:
+            raise ValueError(f"row_budget has {rb.size} entries for {nq} query blocks")
+        rb_dev = torch.as_tensor(rb.astype(np.int32)).to(dev, non_blocking=False)
+        k = row_budgets(nf, nk, budget_mode, ratio, min_budget, rb)
+    else:
+        k = row_budgets(nf, nk, budget_mode, ratio, min_budget)
+    kmax = int(num_txt_blk + (k.max() if nq > 0 else 0))
+    indices = torch.empty((B, NH, nq, kmax), dtype=torch.int32, device=dev)
+    counts = torch.empty((B, NH, nq), dtype=torch.int32, device=dev)
+    scores = torch.empty((B, NH, nq, nk), dtype=q_pool.dtype, device=dev) if return_scores else None
+    p = MaskParams(metric=metric_code, budget_mode=budget_mode, topk_ratio=float(ratio), min_budget=int(min_budget),
+                   n_recent=int(n_recent), force_diag=int(bool(force_diag)), force_sink=int(bool(force_sink)),
+                   force_neighbors=int(bool(force_neighbors)), nq=nq, nk=nk, nh=nh, nw=nw,
+                   num_txt_blk=int(num_txt_blk), kmax=kmax,
+                   row_budget=rb_dev.data_ptr() if rb_dev is not None else None,
+                   scale=float(np.float32(1.0 / math.sqrt(D))))
+    st = lib.li_block_mask(dtype_code(q_pool), B, NH, D, q_pool.data_ptr(), i64_array(q_pool.stride()),
+                           k_pool.data_ptr(), i64_array(k_pool.stride()), ctypes.byref(p), indices.data_ptr(),
+                           counts.data_ptr(), scores.data_ptr() if scores is not None else None, _stream(dev))
+    check("li_block_mask", st)
+    # rb_dev may be released now: the caching allocator reuses it only in stream order.
+    if return_scores:
+        return indices, counts, scores
+    return indices, counts
+
+
+def bsa_forward(q, k, v, indices, counts, sm_scale, block_size, return_lse=False, out=None):
+    """Block-sparse attention over contiguous (B,H,L,D) tensors (see li_bsa_fwd); no host sync."""
+    dev = _device_check(q, k, v, indices, counts)
+    _same_dtype(q, k, v)
+    if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
+        raise ValueError("q, k, v must be contiguous")
+    B, NH, Lq, D = q.shape
+    Lk = k.shape[2]
+    if tuple(k.shape) != (B, NH, Lk, D) or tuple(v.shape) != (B, NH, Lk, D):
+        raise ValueError(f"shape mismatch q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    if indices.dtype != torch.int32 or counts.dtype != torch.int32:
+        raise TypeError("block indices and counts must be int32")
+    nqt = ceil_div(Lq, block_size)
+    if indices.dim() != 4 or tuple(indices.shape[:2]) != (B, NH) or indices.shape[2] < nqt:
+        raise ValueError(f"block_indices shape {tuple(indices.shape)} does not cover {nqt} query tiles")
+    if counts.dim() != 3 or tuple(counts.shape[:2]) != (B, NH) or counts.shape[2] < nqt:
+        raise ValueError(f"block_counts shape {tuple(counts.shape)} does not cover {nqt} query tiles")
+    if out is None:
+        out = torch.empty_like(q)
+    lse = torch.empty((B, NH, Lq), dtype=torch.float32, device=dev) if return_lse else None
+    st = lib.li_bsa_fwd(dtype_code(q), B, NH, Lq, Lk, D, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                        indices.data_ptr(), i64_array(indices.stride()), indices.shape[3], counts.data_ptr(),
+                        i64_array(counts.stride()), float(sm_scale), int(block_size), out.data_ptr(),
+                        lse.data_ptr() if lse is not None else None, _stream(dev))
+    if st == _lib.LI_ERR_K_LEN:
+        raise ValueError(f"K Length ({Lk}) must be divisible by logical_block_size ({block_size})")
+    check("li_bsa_fwd", st)
+    return (out, lse) if return_lse else out

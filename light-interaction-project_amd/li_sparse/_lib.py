@@ -1,0 +1,103 @@
+"""ctypes binding of ``libli_sparse_attn.so`` (the C ABI in include/li_sparse_attn.h).
+
+The library is loaded once, from this package directory.  There is no
+fallback: if it is missing or does not export the ABI, importing this module
+raises ``ImportError`` naming the build command.
+"""
+import ctypes
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libli_sparse_attn.so")
+ABI_VERSION = 1
+
+LI_OK = 0
+LI_ERR_INVALID_ARG = -1
+LI_ERR_SHAPE = -2
+LI_ERR_K_LEN = -3
+LI_ERR_INDEX_RANGE = -4
+LI_ERR_UNSUPPORTED = -5
+LI_ERR_LAUNCH = -6
+LI_ERR_TOO_LARGE = -7
+
+LI_DTYPE_BF16 = 0
+LI_DTYPE_F16 = 1
+
+LI_METRIC_COSINE = 0
+LI_METRIC_SCALED_DOT = 1
+LI_METRIC_DOT = 2
+
+LI_BUDGET_HISTORY = 0
+LI_BUDGET_TOTAL = 1
+
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+
+
+class TileGeom(ctypes.Structure):
+    _fields_ = [("T", _i32), ("H", _i32), ("W", _i32), ("tt", _i32), ("th", _i32), ("tw", _i32),
+                ("nh", _i32), ("nw", _i32)]
+
+
+class MaskParams(ctypes.Structure):
+    _fields_ = [("metric", _i32), ("budget_mode", _i32), ("topk_ratio", ctypes.c_double),
+                ("min_budget", _i32), ("n_recent", _i32), ("force_diag", _i32), ("force_sink", _i32),
+                ("force_neighbors", _i32), ("nq", _i32), ("nk", _i32), ("nh", _i32), ("nw", _i32),
+                ("num_txt_blk", _i32), ("kmax", _i32), ("row_budget", _vp), ("scale", ctypes.c_float)]
+
+
+# name -> (restype, argtypes); mirrors include/li_sparse_attn.h
+SIGNATURES = {
+    "li_abi_version": (ctypes.c_int, []),
+    "li_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "li_q_prep": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+                                 ctypes.POINTER(TileGeom), _vp]),
+    "li_kv_prep": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+                                  _vp, _i64p, _i64, _i64, ctypes.POINTER(TileGeom), _vp]),
+    "li_untile": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p,
+                                 ctypes.POINTER(TileGeom), _vp]),
+    "li_block_mask": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p,
+                                     ctypes.POINTER(MaskParams), _vp, _vp, _vp, _vp]),
+    "li_bsa_fwd": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64p, _i32,
+                                  _vp, _i64p, ctypes.c_float, _i32, _vp, _vp, _vp]),
+}
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run `python light-interaction-project_amd/build_lib.py` "
+                          "(or __graft_entry__.build()) first")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    v = lib.li_abi_version()
+    if v != ABI_VERSION:
+        raise ImportError(f"{LIB_PATH} has ABI version {v}, expected {ABI_VERSION}; rebuild it")
+    return lib
+
+
+lib = _load()
+
+
+def status_string(code):
+    return lib.li_status_string(code).decode()
+
+
+class LiError(RuntimeError):
+    def __init__(self, fn, code):
+        super().__init__(f"{fn} failed: {status_string(code)} (status {code})")
+        self.code = code
+
+
+def check(fn, code):
+    if code != LI_OK:
+        raise LiError(fn, code)
+
+
+def i64_array(vals):
+    vals = list(vals)
+    return (ctypes.c_int64 * len(vals))(*vals)

@@ -1,0 +1,121 @@
+"""The sparse-attention call shared by the HY and MG entry points.
+
+Steps (ar_sparse_operation.py:316-362, bi_sparse_operation_for_KV_cache.py:347-395,
+bi_sparse_operation.py:246-348): block geometry; tile buffers; text K/V
+zero-padded into the leading blocks; Q tile gather + pool; K/V tile gather +
+K pool; block selection; block-sparse attention; untile into ``empty_like(q)``.
+Every stage except the text copy is one HIP kernel of this package; the
+index lists come from the mask kernel, so the attention launch needs no
+host-side range check (the reference's ``block_indices.max()`` sync is gone).
+"""
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from . import _core
+
+
+@dataclass(frozen=True)
+class Geometry:
+    """Block geometry of one call (ar_sparse_operation.py:319-327)."""
+    H: int
+    W: int
+    tt: int
+    th: int
+    tw: int
+    bs: int
+    nh: int
+    nw: int
+    T_q: int
+    T_k: int
+    nt_q: int
+    nt_k: int
+    num_txt_blk: int
+    nq_blk: int
+    nk_blk: int
+
+
+def pad_blocks(x, t):
+    return (x + (t - x % t) % t) // t
+
+
+def geometry(latent_hw, tile, vis_len_q, vis_len_k, text_len):
+    H, W = latent_hw
+    tt, th, tw = tile
+    bs = tt * th * tw
+    nh, nw = pad_blocks(H, th), pad_blocks(W, tw)
+    T_q, T_k = vis_len_q // (H * W), vis_len_k // (H * W)
+    nt_q, nt_k = pad_blocks(T_q, tt), pad_blocks(T_k, tt)
+    num_txt_blk = pad_blocks(text_len, bs)
+    return Geometry(H, W, tt, th, tw, bs, nh, nw, T_q, T_k, nt_q, nt_k, num_txt_blk, nt_q * nh * nw, nt_k * nh * nw)
+
+
+def _stage(events, name):
+    if events is not None:
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        events[name] = e
+
+
+def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, events=None):
+    """One sparse-attention forward.
+
+    q (B,H,Lq,D); k_txt/v_txt (B,H,N_txt,D) or None; k_vis/v_vis (B,H,Lk,D), any strides.
+    ``select(q_pool, k_pool, text_len, grid_q, grid_k) -> (indices, counts)``.
+    ``events`` (dict or None) collects CUDA events per stage for profiling.
+    """
+    out_dtype = q.dtype
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        q, k_vis, v_vis = q.to(torch.bfloat16), k_vis.to(torch.bfloat16), v_vis.to(torch.bfloat16)
+        if k_txt is not None:
+            k_txt, v_txt = k_txt.to(torch.bfloat16), v_txt.to(torch.bfloat16)
+    text_len = 0 if k_txt is None else k_txt.shape[2]
+    g = geometry(latent_hw, tile, q.shape[2], k_vis.shape[2], text_len)
+    B, NH, _, D = q.shape
+    dev, dt = q.device, q.dtype
+    _stage(events, "alloc_start")
+    q_tiled = torch.empty((B, NH, g.nq_blk, g.bs, D), device=dev, dtype=dt)
+    q_pool = torch.empty((B, NH, g.nq_blk, D), device=dev, dtype=dt)
+    k_all = torch.empty((B, NH, g.num_txt_blk + g.nk_blk, g.bs, D), device=dev, dtype=dt)
+    v_all = torch.empty((B, NH, g.num_txt_blk + g.nk_blk, g.bs, D), device=dev, dtype=dt)
+    k_pool = torch.empty((B, NH, g.nk_blk, D), device=dev, dtype=dt)
+    if text_len > 0:
+        pad = g.num_txt_blk * g.bs - text_len
+        kt = F.pad(k_txt, (0, 0, 0, pad)) if pad > 0 else k_txt
+        vt = F.pad(v_txt, (0, 0, 0, pad)) if pad > 0 else v_txt
+        k_all[:, :, :g.num_txt_blk].copy_(kt.reshape(B, NH, g.num_txt_blk, g.bs, D))
+        v_all[:, :, :g.num_txt_blk].copy_(vt.reshape(B, NH, g.num_txt_blk, g.bs, D))
+    _stage(events, "alloc_end")
+    _stage(events, "prep_start")
+    _core.q_prep(q, q_tiled, q_pool, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    _core.kv_prep(k_vis, v_vis, k_all, v_all, k_pool, g.num_txt_blk, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw,
+                  g.nh, g.nw)
+    _stage(events, "prep_end")
+    _stage(events, "index_start")
+    indices, counts = select(q_pool, k_pool, text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
+    _stage(events, "index_end")
+    _stage(events, "attn_start")
+    o_flat = _core.bsa_forward(q_tiled.flatten(2, 3), k_all.flatten(2, 3), v_all.flatten(2, 3), indices, counts,
+                               1.0 / math.sqrt(D), g.bs)
+    _stage(events, "attn_end")
+    _stage(events, "untile_start")
+    o_out = torch.empty_like(q)
+    _core.untile(o_flat.view(B, NH, g.nq_blk, g.bs, D), o_out, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    _stage(events, "untile_end")
+    return o_out if o_out.dtype == out_dtype else o_out.to(out_dtype)
+
+
+def recent_blocks(params, tt, nh, nw, nk):
+    """Trailing key blocks protected by ``recent_protect`` frames (ar_sparse_operation.py:263-266)."""
+    rp = params.get("recent_protect", 0)
+    if rp > 0:
+        return min(((rp + tt - 1) // tt) * nh * nw, nk)
+    return 0
+
+
+def extras(params):
+    """Forced-block and ragged-budget extensions (unset = the reference's rules)."""
+    return dict(force_diag=bool(params.get("force_diag", False)), force_sink=bool(params.get("force_sink", False)),
+                row_budget=params.get("row_budget"))

@@ -1,0 +1,108 @@
+"""GPU parity: block-mask builder vs the oracle (bit-exact scores, indices, counts) and the golden fixtures."""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits, from_bits, oracle_forced
+from li_sparse import _core, _lib
+from li_sparse.hy.ar_sparse_operation import fast_generate_indices
+from li_sparse.hy.bi_sparse_operation_for_KV_cache import generate_prefill_indices
+from li_sparse.workloads import WORKLOADS, make_qkv
+from oracle import mask as omask
+from oracle import tile as otile
+from oracle.geometry import block_geometry
+from test_oracle_mask import CASES
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "mask_golden.npz")
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_golden_cases_bit_exact(dev, name):
+    print(f"[gpu] mask golden {name}", flush=True)
+    g = np.load(GOLDEN)
+    mode, (nt_q, nt_k, nh, nw), text_len, params = CASES[name]
+    qp, kp = g[f"{name}/q_pool"], g[f"{name}/k_pool"]
+    qd, kd = from_bits(qp).to(dev), from_bits(kp).to(dev)
+    if mode == "decode":
+        ind, cnt = fast_generate_indices(qd, kd, text_len, (nt_q, nh, nw), (nt_k, nh, nw), params, dev)
+        oind, ocnt = omask.fast_generate_indices(qp, kp, text_len, (nt_q, nh, nw), (nt_k, nh, nw), params)
+    else:
+        ind, cnt = generate_prefill_indices(qd, kd, text_len, (nt_k, nh, nw), params, dev)
+        oind, ocnt = omask.generate_prefill_indices(qp, kp, text_len, (nt_k, nh, nw), params)
+    torch.cuda.synchronize()
+    assert np.array_equal(ind.cpu().numpy(), oind)
+    assert np.array_equal(cnt.cpu().numpy(), ocnt)
+    tf = g[f"{name}/tie_free"]
+    assert np.array_equal(ind.cpu().numpy()[tf], g[f"{name}/indices"][tf])
+
+
+@pytest.mark.parametrize("name", ["toy", "hy", "mg", "hy_long"])
+def test_workload_selection_bit_exact(dev, name):
+    wl = WORKLOADS[name]
+    print(f"[gpu] mask workload {name}", flush=True)
+    q, k, _ = make_qkv(wl, seed=3)
+    geo = block_geometry(wl.lq, wl.lk, wl.latent_hw, wl.tile)
+    H, W = wl.latent_hw
+    qp = otile.pool_mean(otile.tile_gather(bits(q), geo["T_q"], H, W, wl.tile))
+    kp = otile.pool_mean(otile.tile_gather(bits(k), geo["T_k"], H, W, wl.tile))
+    params = wl.sparse_params(geo["nq_blk"])
+    forced, kk = oracle_forced(geo, params, "decode")
+    oind, ocnt, oscore, tf = omask.build_indices(qp, kp, metric=wl.metric, forced=forced, k=kk, num_txt_blk=0)
+    ind, cnt, sc = _core.block_mask(from_bits(qp).to(dev), from_bits(kp).to(dev), metric=wl.metric,
+                                    budget_mode=_lib.LI_BUDGET_HISTORY, ratio=wl.ratio, nh=geo["nh"], nw=geo["nw"],
+                                    force_diag=True, force_sink=True, row_budget=params.get("row_budget"),
+                                    return_scores=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(sc), oscore)
+    assert np.array_equal(cnt.cpu().numpy(), ocnt)
+    assert np.array_equal(ind.cpu().numpy(), oind)
+    print(f"[gpu]   rows tie-free (>= 2 bf16 ulps at the cut): {tf.mean():.3f}", flush=True)
+
+
+@pytest.mark.parametrize("metric", ["cosine", "scaled_dot_product", "dot"])
+@pytest.mark.parametrize("rule", ["recent", "prefill", "ragged"])
+def test_rules_and_metrics(dev, metric, rule):
+    print(f"[gpu] mask rule={rule} metric={metric}", flush=True)
+    rng = np.random.default_rng(sum(map(ord, metric + rule)))
+    nh, nw, nt_q, nt_k, D = 3, 5, 2, 6, 128
+    if rule == "prefill":
+        nt_q = nt_k
+    nq, nk = nt_q * nh * nw, nt_k * nh * nw
+    qp = torch.randn(2, 3, nq, D, generator=torch.Generator().manual_seed(rng.integers(1 << 30))).to(torch.bfloat16)
+    kp = torch.randn(2, 3, nk, D, generator=torch.Generator().manual_seed(rng.integers(1 << 30))).to(torch.bfloat16)
+    if rule == "recent":
+        params = {"tile_size": (2, 8, 8), "topk_ratio": 0.2, "recent_protect": 4, "sim_metric": metric}
+        ind, cnt = fast_generate_indices(qp.to(dev), kp.to(dev), 130, (nt_q, nh, nw), (nt_k, nh, nw), params, dev)
+        oind, ocnt = omask.fast_generate_indices(bits(qp), bits(kp), 130, (nt_q, nh, nw), (nt_k, nh, nw), params)
+    elif rule == "prefill":
+        params = {"tile_size": (4, 4, 8), "topk_ratio": 0.25, "sim_metric": metric}
+        ind, cnt = generate_prefill_indices(qp.to(dev), kp.to(dev), 0, (nt_k, nh, nw), params, dev)
+        oind, ocnt = omask.generate_prefill_indices(bits(qp), bits(kp), 0, (nt_k, nh, nw), params)
+    else:
+        rb = rng.integers(0, nk + 5, size=nq).tolist()
+        params = {"tile_size": (2, 8, 8), "topk_ratio": 0.1, "sim_metric": metric, "force_diag": True,
+                  "force_sink": True, "row_budget": rb}
+        ind, cnt = fast_generate_indices(qp.to(dev), kp.to(dev), 0, (nt_q, nh, nw), (nt_k, nh, nw), params, dev)
+        oind, ocnt = omask.fast_generate_indices(bits(qp), bits(kp), 0, (nt_q, nh, nw), (nt_k, nh, nw), params)
+    torch.cuda.synchronize()
+    assert np.array_equal(cnt.cpu().numpy(), ocnt)
+    assert np.array_equal(ind.cpu().numpy(), oind)
+
+
+def test_five_d_input_and_ties(dev):
+    # tiled (5-D) input is mean-pooled first; all-equal pools -> every score ties -> lower indices win
+    print("[gpu] mask 5-D input + all ties", flush=True)
+    nh, nw = 2, 2
+    x = torch.ones(1, 1, 8, 16, 64, dtype=torch.bfloat16, device=dev)
+    params = {"tile_size": (1, 4, 4), "topk_ratio": 0.3, "sim_metric": "dot"}
+    ind, cnt = generate_prefill_indices(x, x, 0, (2, nh, nw), params, dev)
+    torch.cuda.synchronize()
+    forced = omask.forced_mask(8, 8, nh, nw, neighbors=True)
+    for r in range(8):
+        free = [j for j in range(8) if not forced[r, j]]
+        want = sorted(list(np.nonzero(forced[r])[0]) + free[:max(0, 7 - int(forced[r].sum()))])
+        assert ind[0, 0, r].tolist() == want
