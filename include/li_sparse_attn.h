@@ -52,6 +52,8 @@ typedef struct li_tile_geom {
 int li_abi_version(void);
 /* Static text for a status code. */
 const char* li_status_string(int status);
+/* HIP error name and text of the calling thread's last failed launch (LI_ERR_LAUNCH). */
+const char* li_last_error(void);
 
 /*
  * Q tile gather + mean pool.  Replaces launch_q_prep(src, dst, mean, T, H, W,

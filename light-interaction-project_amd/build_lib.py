@@ -23,6 +23,8 @@ ARCH = "gfx950"
 CFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
     "-I", os.path.join(REPO, "include"), "-I", CSRC,
+    # code object v5 loads in every ROCm 7.x runtime, including the one torch ships
+    "-mcode-object-version=5",
     # packed fp32 VALU ops stay disabled for all device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",

@@ -1,5 +1,17 @@
-// Version and status strings of the sparse-attention C ABI.
+// Version, status strings and the last launch error of the sparse-attention C ABI.
+#include <stdio.h>
+
 #include "li_common.hpp"
+
+namespace {
+thread_local char g_last_error[256] = "no launch error";
+}
+
+void li::record_launch_error(hipError_t e) {
+  snprintf(g_last_error, sizeof(g_last_error), "%s: %s", hipGetErrorName(e), hipGetErrorString(e));
+}
+
+extern "C" const char* li_last_error(void) { return g_last_error; }
 
 extern "C" int li_abi_version(void) { return 1; }
 

@@ -368,6 +368,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_kernel(BsaArgs a) {
 
 template <typename E, int BS, int D>
 int launch_bsa(BsaArgs& a, int tiles, hipStream_t s) {
+  clear_launch_error();
   hipLaunchKernelGGL((bsa_fwd_kernel<E, BS, D>), dim3(tiles), dim3(Cfg<BS, D>::NTHR), 0, s, a);
   return launch_status();
 }

@@ -43,10 +43,19 @@ struct F16 {
 
 __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) { return uint32_t(lo) | (uint32_t(hi) << 16); }
 
-// Launch status helper.
+// Launch status: call clear_launch_error() right before a kernel launch and
+// launch_status() right after it, so an error left by an earlier, unrelated
+// runtime call is not attributed to this launch.  The text of a failed
+// launch is kept per thread for li_last_error().
+void record_launch_error(hipError_t e);
+
+inline void clear_launch_error() { (void)hipGetLastError(); }
+
 inline int launch_status() {
   hipError_t e = hipGetLastError();
-  return e == hipSuccess ? LI_OK : LI_ERR_LAUNCH;
+  if (e == hipSuccess) return LI_OK;
+  record_launch_error(e);
+  return LI_ERR_LAUNCH;
 }
 
 }  // namespace li

@@ -248,6 +248,7 @@ extern "C" int li_block_mask(int dtype, int32_t B, int32_t NH, int32_t D, const 
   const size_t lds = (size_t)p.nk * 4 + (size_t)p.nk + 16;
   dim3 grid((unsigned)p.nq, (unsigned)(B * NH));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  clear_launch_error();
   if (dtype == LI_DTYPE_BF16 && D == 128)
     hipLaunchKernelGGL((block_mask_kernel<Bf16, 128>), grid, dim3(256), lds, s, a);
   else if (dtype == LI_DTYPE_BF16 && D == 64)

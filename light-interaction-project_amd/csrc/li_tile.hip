@@ -191,6 +191,7 @@ int launch_gather(int dtype, int32_t B, int32_t NH, int32_t D, GatherArgs& a, co
   a.bs = geom->tt * geom->th * geom->tw;
   a.g = *geom;
   dim3 grid((unsigned)nblk, (unsigned)(B * NH));
+  clear_launch_error();
   if (dtype == LI_DTYPE_BF16 && D == 128)
     hipLaunchKernelGGL((gather_pool_kernel<Bf16, 128, NT>), grid, dim3(256), 0, stream, a);
   else if (dtype == LI_DTYPE_BF16 && D == 64)
@@ -280,6 +281,7 @@ extern "C" int li_untile(int dtype, int32_t B, int32_t NH, int32_t D, const void
   a.vec_dst = vec_ok(dst, dst_strides, 4);
   dim3 grid((unsigned)nblk, (unsigned)(B * NH));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  clear_launch_error();
   if (D == 128)
     hipLaunchKernelGGL(untile_kernel<128>, grid, dim3(256), 0, s, a);
   else if (D == 64)

@@ -3,9 +3,17 @@
 The library is loaded once, from this package directory.  There is no
 fallback: if it is missing or does not export the ABI, importing this module
 raises ``ImportError`` naming the build command.
+
+torch is imported first so that the HIP runtime torch ships with is already
+mapped when the library is loaded: the library's ``libamdhip64.so.7``
+dependency then resolves (by SONAME) to that same runtime, and torch's
+streams and device pointers are valid in the library's launches.  Loading
+the library first would map a second, independent HIP runtime.
 """
 import ctypes
 import os
+
+import torch  # noqa: F401  (must precede the CDLL below)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libli_sparse_attn.so")
 ABI_VERSION = 1
@@ -52,6 +60,7 @@ class MaskParams(ctypes.Structure):
 SIGNATURES = {
     "li_abi_version": (ctypes.c_int, []),
     "li_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "li_last_error": (ctypes.c_char_p, []),
     "li_q_prep": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p, _vp, _i64p,
                                  ctypes.POINTER(TileGeom), _vp]),
     "li_kv_prep": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
@@ -89,7 +98,10 @@ def status_string(code):
 
 class LiError(RuntimeError):
     def __init__(self, fn, code):
-        super().__init__(f"{fn} failed: {status_string(code)} (status {code})")
+        msg = f"{fn} failed: {status_string(code)} (status {code})"
+        if code == LI_ERR_LAUNCH:
+            msg += f": {lib.li_last_error().decode()}"
+        super().__init__(msg)
         self.code = code
 
 

@@ -75,3 +75,15 @@ def test_oracle_is_not_imported_by_the_product():
                 src = open(os.path.join(root, f)).read()
                 assert not re.search(r"^\s*(from|import)\s+oracle", src, flags=re.M), f
     assert "oracle" not in {m.split(".")[0] for m in sys.modules if m.startswith("li_sparse")}
+
+
+def test_single_hip_runtime_is_mapped():
+    # The library must bind to the HIP runtime torch loaded (one libamdhip64 in the process);
+    # two runtimes would make torch's streams and pointers foreign to the library's launches.
+    import torch  # noqa: F401
+
+    maps = open("/proc/self/maps").read()
+    libs = {line.split()[-1] for line in maps.splitlines() if "libamdhip64" in line}
+    assert len(libs) == 1, libs
+    ours = os.path.realpath(L.LIB_PATH)
+    assert any(os.path.realpath(line.split()[-1]) == ours for line in maps.splitlines() if "libli_sparse" in line)

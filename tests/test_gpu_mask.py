@@ -72,8 +72,8 @@ def test_rules_and_metrics(dev, metric, rule):
     if rule == "prefill":
         nt_q = nt_k
     nq, nk = nt_q * nh * nw, nt_k * nh * nw
-    qp = torch.randn(2, 3, nq, D, generator=torch.Generator().manual_seed(rng.integers(1 << 30))).to(torch.bfloat16)
-    kp = torch.randn(2, 3, nk, D, generator=torch.Generator().manual_seed(rng.integers(1 << 30))).to(torch.bfloat16)
+    qp = torch.randn(2, 3, nq, D, generator=torch.Generator().manual_seed(int(rng.integers(1 << 30)))).to(torch.bfloat16)
+    kp = torch.randn(2, 3, nk, D, generator=torch.Generator().manual_seed(int(rng.integers(1 << 30)))).to(torch.bfloat16)
     if rule == "recent":
         params = {"tile_size": (2, 8, 8), "topk_ratio": 0.2, "recent_protect": 4, "sim_metric": metric}
         ind, cnt = fast_generate_indices(qp.to(dev), kp.to(dev), 130, (nt_q, nh, nw), (nt_k, nh, nw), params, dev)
