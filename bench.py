@@ -36,6 +36,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=16, help="heads timed for the CPU baseline sample")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--profile", action="store_true",
+                    help="launch each kernel of the call --steps times (and a 256 MiB copy for counter "
+                         "calibration) for rocprofv3, then print per-launch algorithmic bytes/FLOPs")
     return ap.parse_args()
 
 
@@ -118,6 +121,10 @@ def main():
     attn_ms, attn_per = event_loop(attn, args.steps, stream)
     attn_tflops = flops / (attn_ms * 1e-3) / 1e12
 
+    if args.profile:
+        profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params, ind, cnt, flops, dev)
+        return
+
     # Dense comparators: torch SDPA (valid tokens) and this kernel with every block kept.
     sdpa = lambda: torch.nn.functional.scaled_dot_product_attention(qd, kd, vd)  # noqa: E731
     for _ in range(3):
@@ -171,6 +178,42 @@ def main():
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(wl, q, k, v, counts, ind.cpu().numpy(), g, args.cpu_heads, flops)
     print(json.dumps(result), flush=True)
+
+
+def profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params, ind, cnt, flops, dev):
+    """Each kernel of one call, --steps launches apiece, for rocprofv3 kernel traces and counters."""
+    import torch
+
+    from li_sparse import _core
+    from li_sparse.hy.ar_sparse_operation import fast_generate_indices
+
+    B, H, D, bs = wl.batch, wl.heads, wl.head_dim, g.bs
+    qf, kf, vf = q_t.flatten(2, 3), k_all.flatten(2, 3), v_all.flatten(2, 3)
+    out = torch.empty_like(qf)
+    o_lin = torch.empty_like(qd)
+    src = torch.empty(1 << 27, dtype=torch.bfloat16, device=dev).fill_(1.0)   # 256 MiB
+    dst = torch.empty_like(src)
+    for _ in range(args.steps):
+        _core.bsa_forward(qf, kf, vf, ind, cnt, 1.0 / math.sqrt(D), bs, out=out)
+        _core.q_prep(qd, q_t, q_p, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+        _core.kv_prep(kd, vd, k_all, v_all, k_p, 0, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+        fast_generate_indices(q_p, k_p, 0, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), params, dev)
+        _core.untile(out.view(B, H, g.nq_blk, bs, D), o_lin, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e = 2  # bytes per element
+    print(json.dumps({
+        "profile": wl.name, "launches_per_kernel": args.steps,
+        "algorithmic_per_launch": {
+            "bsa_fwd_kernel": {"flop": flops,
+                               "bytes_min": e * (wl.lq + 2 * wl.lk) * H * D * B,
+                               "note": "FLOPs = sum(counts) * 4 * BS^2 * D; bytes_min = Q + K + V read once"},
+            "gather_pool_kernel<1> (Q)": {"bytes": e * H * D * B * (wl.lq + g.nq_blk * bs) + e * H * D * g.nq_blk},
+            "gather_pool_kernel<2> (K,V)": {"bytes": e * H * D * B * 2 * (wl.lk + g.nk_blk * bs)
+                                            + e * H * D * g.nk_blk},
+            "untile_kernel": {"bytes": e * H * D * B * 2 * wl.lq},
+            "copy (calibration)": {"bytes_read": src.numel() * e, "bytes_written": dst.numel() * e},
+        }}), flush=True)
 
 
 def cpu_baseline(wl, q, k, v, counts, ind, g, n_heads, flops, min_seconds=10.0):

@@ -22,12 +22,27 @@
 //    the whole tile).  Its accumulator layout puts one query per lane
 //    column, so the softmax row statistics need a single cross-half
 //    exchange, and the probabilities feed O^T = V^T P^T directly as the MFMA
-//    B operand without an LDS round trip.
-//  * K and V tiles are double-buffered in LDS: block i+1 is fetched into
-//    registers while block i is computed, then written to the other stage.
-//    K keeps its row layout with a 16-byte-granule XOR swizzle; V is written
-//    transposed (V^T, keys contiguous) with an 8-byte-granule XOR swizzle, so
-//    both MFMA operand reads are bank-conflict free.
+//    B operand without an LDS round trip.  The A operand reads K rows in the
+//    order perm(i) (bits 2 and 3 of the row index swapped): the softmax does
+//    not care about key order, and with it each lane's 8 probabilities of a
+//    16-key MFMA step are 8 consecutive keys, so the matching V^T operand is
+//    two transposing LDS reads of 4 consecutive keys each (below).
+//  * K and V tiles are double-buffered in LDS in their natural [key][d]
+//    layout: block i+1 is fetched into registers while block i is computed,
+//    then copied to the other stage with 16-byte stores.  The V^T operand is
+//    read with gfx950's transposing LDS load (ds_read_b64_tr_b16): in each
+//    16-lane group, lane t supplies V[key0 + t/4][d0 + 4*(t%4) .. +3] and lane
+//    u receives V[key0 + j][d0 + u] for j = 0..3, i.e. four consecutive keys
+//    of its own d row; two such loads give the 8 keys of one MFMA step.
+//    K rows are padded to D+8 elements and V rows to D+32, which makes the K
+//    operand reads and the transposing V reads bank-conflict free (LDS serves
+//    16 lanes of a 16-byte access, or four 64-byte row segments of a
+//    transposing access, per clock) and keeps every LDS address a per-lane
+//    base plus a constant offset.
+//  * Rescaling is lazy: the running max used for the exponentials is only
+//    raised (and O, l rescaled) when a row's block max exceeds it by more
+//    than 8 in log2 units, so probabilities stay <= 2^8 and most blocks skip
+//    the rescale.  The result is the same softmax.
 //  * Workgroup ids are remapped so that each XCD (ids are dealt round-robin
 //    over the 8 XCDs) processes a contiguous range of (head, tile) work and
 //    the tiles of one head share that XCD's L2 for their K/V blocks.
@@ -54,47 +69,66 @@ template <int BS, int D>
 struct Cfg {
   static constexpr int WAVES = 2 * (BS / 32);
   static constexpr int NTHR = 64 * WAVES;
-  static constexpr int QW = 32;           // query rows per wave
   static constexpr int KW = BS / 2;       // keys per wave per block
-  static constexpr int NQT = QW / 32;     // 32-query sub-tiles per wave
   static constexpr int NKT = KW / 32;     // 32-key sub-tiles per wave
   static constexpr int DS = D / 16;       // MFMA k-steps of S (over d)
   static constexpr int NDT = D / 32;      // 32-wide d tiles of O
   static constexpr int PST = KW / 16;     // MFMA k-steps of P V (over keys)
   static constexpr int KGR = D / 8;       // 16-byte granules per K row
-  static constexpr int KSW = (KGR < 16 ? KGR : 16) - 1;  // K swizzle mask
-  static constexpr int VGR = BS / 4;      // 8-byte granules (4 keys) per V^T row
-  static constexpr int K_UNITS = BS * KGR;          // 16-byte K loads per block
-  static constexpr int V_UNITS = (BS / 4) * KGR;    // (4 keys x 8 d) V units per block
-  static constexpr int K_IT = (K_UNITS + NTHR - 1) / NTHR;
-  static constexpr int V_IT = (V_UNITS + NTHR - 1) / NTHR;
-  static constexpr int STAGE_ELEMS = BS * D;        // per K or V^T stage
-  static constexpr int KV_BYTES = 2 * 2 * STAGE_ELEMS * 2;
-  static constexpr int NQW = WAVES / 2;                         // query groups
-  static constexpr int X_FLOATS = NQW * NDT * NQT * 16 * 64;     // epilogue O exchange
-  static constexpr int X_BYTES = X_FLOATS * 4 + NQW * 2 * NQT * 64 * 4;
+  static constexpr int KP = D + 8;        // K row pitch (elements)
+  static constexpr int VP = D + 32;       // V row pitch (elements)
+  static constexpr int K_STAGE = BS * KP;
+  static constexpr int V_STAGE = BS * VP;
+  static constexpr int UNITS = BS * KGR;            // 16-byte loads per K (or V) block
+  static constexpr int IT = (UNITS + NTHR - 1) / NTHR;
+  static constexpr int KV_BYTES = 2 * (K_STAGE + V_STAGE) * 2;
+  static constexpr int NQW = WAVES / 2;                      // query groups
+  static constexpr int X_FLOATS = NQW * NDT * 16 * 64;       // epilogue O exchange
+  static constexpr int X_BYTES = X_FLOATS * 4 + NQW * 2 * 64 * 4;
   static constexpr int LDS_BYTES = KV_BYTES > X_BYTES ? KV_BYTES : X_BYTES;
 };
 
-__device__ __forceinline__ int vswz(int d, int vgr) { return ((d & (vgr - 1)) ^ (d / vgr)) & (vgr - 1); }
+// MFMA row i of the score tile reads K row perm(i): bits 2 and 3 swapped.
+__device__ __forceinline__ int kperm(int i) { return (i & 0x13) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
-__device__ __forceinline__ uint32_t lo_pair(uint32_t a, uint32_t b) {
-  return __builtin_amdgcn_perm(b, a, 0x05040100u);  // {a.lo16, b.lo16}
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Transposing LDS load (ds_read_b64_tr_b16) of 4 x 16-bit elements.
+__device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p)));
 }
-__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
-  return __builtin_amdgcn_perm(b, a, 0x07060302u);  // {a.hi16, b.hi16}
+
+template <typename E>
+__device__ __forceinline__ uint32_t cvt_pk(float a, float b);
+template <>
+__device__ __forceinline__ uint32_t cvt_pk<Bf16>(float a, float b) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), h2));
 }
+template <>
+__device__ __forceinline__ uint32_t cvt_pk<F16>(float a, float b) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), h2));
+}
+
+template <int N>
+struct Stage {
+  static constexpr int value = N;
+};
 
 template <typename E, int BS, int D>
 __global__ __launch_bounds__(4 * BS) void bsa_fwd_kernel(BsaArgs a) {
   using C = Cfg<BS, D>;
   typedef typename E::vec8 vec8;
   __shared__ __attribute__((aligned(16))) char smem[C::LDS_BYTES];
-  uint16_t* kbuf = reinterpret_cast<uint16_t*>(smem);               // [2][BS][D] swizzled
-  uint16_t* vbuf = kbuf + 2 * C::STAGE_ELEMS;                        // [2][D][BS] transposed, swizzled
+  uint16_t* kbuf = reinterpret_cast<uint16_t*>(smem);          // [2][BS][KP]
+  uint16_t* vbuf = kbuf + 2 * C::K_STAGE;                       // [2][BS][VP]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int qh = wave >> 1, kh = wave & 1;
+  const int qq = wave >> 1, kh = wave & 1;
   const int l32 = lane & 31, hl = lane >> 5;
 
   // XCD-aware remap: hardware deals workgroup ids round-robin over 8 XCDs;
@@ -129,239 +163,191 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_kernel(BsaArgs a) {
   }
 
   // Q^T fragments (MFMA B operand): lane holds query row (l32) and d = 16 s + 8 hl .. +7.
-  vec8 qf[C::NQT][C::DS];
-#pragma unroll
-  for (int qt = 0; qt < C::NQT; ++qt) {
-    const int r = row0 + C::QW * qh + 32 * qt + l32;
+  vec8 qf[C::DS];
+  {
+    const int r = row0 + 32 * qq + l32;
 #pragma unroll
     for (int s = 0; s < C::DS; ++s) {
       u32x4 x = {0u, 0u, 0u, 0u};
       if (r < a.Lq) x = *reinterpret_cast<const u32x4*>(qhead + (int64_t)r * D + 16 * s + 8 * hl);
-      qf[qt][s] = __builtin_bit_cast(vec8, x);
+      qf[s] = __builtin_bit_cast(vec8, x);
     }
   }
 
-  u32x4 kst[C::K_IT];
-  u32x4 vst[C::V_IT][4];
+  // Per-lane LDS element offsets (stage 0); stage 1 adds K_STAGE / V_STAGE.
+  int k_rd[C::NKT];
+#pragma unroll
+  for (int kt = 0; kt < C::NKT; ++kt) k_rd[kt] = (C::KW * kh + 32 * kt + kperm(l32)) * C::KP + 8 * hl;
+  // Transposing V read: lane t of each 16-lane group g points at key
+  // (KW*kh + 8*hl + t/4) and d = 16*(g&1) + 4*(t%4) of the block.
+  const int t16 = lane & 15, g16 = lane >> 4;
+  const int v_tr = (C::KW * kh + 8 * hl + (t16 >> 2)) * C::VP + 16 * (g16 & 1) + 4 * (t16 & 3);
+
+  u32x4 kst[C::IT];
+  u32x4 vst[C::IT];
   auto fetch = [&](int blk) {
     const uint16_t* kb = khead + (int64_t)blk * BS * D;
     const uint16_t* vb = vhead + (int64_t)blk * BS * D;
 #pragma unroll
-    for (int it = 0; it < C::K_IT; ++it) {
+    for (int it = 0; it < C::IT; ++it) {
       const int u = tid + C::NTHR * it;
-      if (C::K_UNITS % C::NTHR == 0 || u < C::K_UNITS)
+      if (C::UNITS % C::NTHR == 0 || u < C::UNITS) {
         kst[it] = *reinterpret_cast<const u32x4*>(kb + (u / C::KGR) * D + 8 * (u % C::KGR));
-    }
-#pragma unroll
-    for (int it = 0; it < C::V_IT; ++it) {
-      const int u = tid + C::NTHR * it;
-      if (C::V_UNITS % C::NTHR == 0 || u < C::V_UNITS) {
-        const int q4 = u / C::KGR, c = u % C::KGR;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          vst[it][e] = *reinterpret_cast<const u32x4*>(vb + (4 * q4 + e) * D + 8 * c);
+        vst[it] = *reinterpret_cast<const u32x4*>(vb + (u / C::KGR) * D + 8 * (u % C::KGR));
       }
     }
   };
-  auto stash = [&](int stage) {
-    uint16_t* kd = kbuf + stage * C::STAGE_ELEMS;
-    uint16_t* vd = vbuf + stage * C::STAGE_ELEMS;
+  auto stash = [&](auto stage) {
+    constexpr int ST = decltype(stage)::value;
+    uint16_t* kd = kbuf + ST * C::K_STAGE;
+    uint16_t* vd = vbuf + ST * C::V_STAGE;
 #pragma unroll
-    for (int it = 0; it < C::K_IT; ++it) {
+    for (int it = 0; it < C::IT; ++it) {
       const int u = tid + C::NTHR * it;
-      if (C::K_UNITS % C::NTHR == 0 || u < C::K_UNITS) {
-        const int key = u / C::KGR, g = u % C::KGR;
-        *reinterpret_cast<u32x4*>(kd + key * D + 8 * (g ^ (key & C::KSW))) = kst[it];
-      }
-    }
-#pragma unroll
-    for (int it = 0; it < C::V_IT; ++it) {
-      const int u = tid + C::NTHR * it;
-      if (C::V_UNITS % C::NTHR == 0 || u < C::V_UNITS) {
-        const int q4 = u / C::KGR, c = u % C::KGR;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int d = 8 * c + i;
-          const int wd = i >> 1;
-          u32x2 word;
-          if (i & 1) {
-            word[0] = hi_pair(vst[it][0][wd], vst[it][1][wd]);
-            word[1] = hi_pair(vst[it][2][wd], vst[it][3][wd]);
-          } else {
-            word[0] = lo_pair(vst[it][0][wd], vst[it][1][wd]);
-            word[1] = lo_pair(vst[it][2][wd], vst[it][3][wd]);
-          }
-          *reinterpret_cast<u32x2*>(vd + d * BS + 4 * (q4 ^ vswz(d, C::VGR))) = word;
-        }
+      if (C::UNITS % C::NTHR == 0 || u < C::UNITS) {
+        *reinterpret_cast<u32x4*>(kd + (u / C::KGR) * C::KP + 8 * (u % C::KGR)) = kst[it];
+        *reinterpret_cast<u32x4*>(vd + (u / C::KGR) * C::VP + 8 * (u % C::KGR)) = vst[it];
       }
     }
   };
 
-  f32x16 o[C::NDT][C::NQT];
+  f32x16 o[C::NDT];
 #pragma unroll
   for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
-    for (int qt = 0; qt < C::NQT; ++qt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[dt][qt][r] = 0.0f;
-  float mrow[C::NQT], lrow[C::NQT];
-#pragma unroll
-  for (int qt = 0; qt < C::NQT; ++qt) {
-    mrow[qt] = -__builtin_inff();
-    lrow[qt] = 0.0f;
-  }
+    for (int r = 0; r < 16; ++r) o[dt][r] = 0.0f;
+  float mrow = -__builtin_inff(), lrow = 0.0f;
   const float qk_scale = a.qk_scale;
 
-  auto block_id = [&](int i) {
-    int id = __builtin_amdgcn_readfirstlane(irow[(int64_t)i * a.is[3]]);
-    return id;
+  auto compute = [&](auto stage) {
+    constexpr int ST = decltype(stage)::value;
+    const uint16_t* kd = kbuf + ST * C::K_STAGE;
+    const uint16_t* vd = vbuf + ST * C::V_STAGE;
+    // S^T = K Q^T for this wave's key half.
+    f32x16 sacc[C::NKT];
+#pragma unroll
+    for (int kt = 0; kt < C::NKT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < C::DS; ++s) {
+#pragma unroll
+      for (int kt = 0; kt < C::NKT; ++kt) {
+        const vec8 ka = __builtin_bit_cast(vec8, *reinterpret_cast<const u32x4*>(kd + k_rd[kt] + 16 * s));
+        sacc[kt] = E::mfma32(ka, qf[s], sacc[kt]);
+      }
+    }
+    // Online softmax: lane owns query column l32; the other half of the
+    // wave's keys for that query sits in lane ^ 32.
+    float mx = sacc[0][0];
+#pragma unroll
+    for (int kt = 0; kt < C::NKT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, sacc[kt][r]);
+    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32)) * qk_scale;
+    if (__ballot(mx > mrow + 8.0f)) {
+      const float mnew = __builtin_fmaxf(mrow, mx);
+      const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+      mrow = mnew;
+      lrow *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    }
+    float ls = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < C::NKT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][r], qk_scale, -mrow));
+        sacc[kt][r] = pv;
+        ls += pv;
+      }
+    lrow += ls;
+    // O^T += V^T P^T, one 16-key step at a time.
+#pragma unroll
+    for (int st = 0; st < C::PST; ++st) {
+      const int kt = st >> 1, ip = st & 1;
+      u32x4 pk;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pk[e] = cvt_pk<E>(sacc[kt][8 * ip + 2 * e], sacc[kt][8 * ip + 2 * e + 1]);
+      const vec8 pf = __builtin_bit_cast(vec8, pk);
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt) {
+        const uint16_t* pv = vd + v_tr + (32 * kt + 16 * ip) * C::VP + 32 * dt;
+        const u32x2 lo = lds_read_tr(pv);               // keys +0..3 of the step's 8
+        const u32x2 hi = lds_read_tr(pv + 4 * C::VP);   // keys +4..7
+        const vec8 va = __builtin_bit_cast(vec8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        o[dt] = E::mfma32(va, pf, o[dt]);
+      }
+    }
   };
 
-  int cur = block_id(0);
-  fetch(((unsigned)cur < (unsigned)a.nkb) ? cur : 0);
-  stash(0);
-  __syncthreads();
+  auto block_id = [&](int i) { return __builtin_amdgcn_readfirstlane(irow[(int64_t)i * a.is[3]]); };
+  auto valid = [&](int id_) { return (unsigned)id_ < (unsigned)a.nkb; };
 
-  for (int i = 0; i < count; ++i) {
-    const int stage = i & 1;
+  // One block per step: prefetch the next block into registers, compute the
+  // current stage, then write the prefetched block to the other stage.
+  auto step = [&](auto stage, int i, int& cur) {
+    constexpr int ST = decltype(stage)::value;
     int nxt = 0;
     if (i + 1 < count) {
       nxt = block_id(i + 1);
-      fetch(((unsigned)nxt < (unsigned)a.nkb) ? nxt : 0);
+      fetch(valid(nxt) ? nxt : 0);
     }
-    if ((unsigned)cur < (unsigned)a.nkb) {
-      const uint16_t* kd = kbuf + stage * C::STAGE_ELEMS;
-      const uint16_t* vd = vbuf + stage * C::STAGE_ELEMS;
-      // S^T = K Q^T for this wave's key half.
-      f32x16 sacc[C::NKT][C::NQT];
-#pragma unroll
-      for (int kt = 0; kt < C::NKT; ++kt)
-#pragma unroll
-        for (int qt = 0; qt < C::NQT; ++qt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) sacc[kt][qt][r] = 0.0f;
-#pragma unroll
-      for (int s = 0; s < C::DS; ++s) {
-        vec8 ka[C::NKT];
-#pragma unroll
-        for (int kt = 0; kt < C::NKT; ++kt) {
-          const int key = C::KW * kh + 32 * kt + l32;
-          const int g = 2 * s + hl;
-          ka[kt] = __builtin_bit_cast(vec8, *reinterpret_cast<const u32x4*>(kd + key * D + 8 * (g ^ (key & C::KSW))));
-        }
-#pragma unroll
-        for (int kt = 0; kt < C::NKT; ++kt)
-#pragma unroll
-          for (int qt = 0; qt < C::NQT; ++qt) sacc[kt][qt] = E::mfma32(ka[kt], qf[qt][s], sacc[kt][qt]);
-      }
-      // Online softmax: lane owns query column l32 of each sub-tile; the other
-      // half of the wave's keys for that query sits in lane ^ 32.
-#pragma unroll
-      for (int qt = 0; qt < C::NQT; ++qt) {
-        float mx = sacc[0][qt][0];
-#pragma unroll
-        for (int kt = 0; kt < C::NKT; ++kt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, sacc[kt][qt][r]);
-        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
-        const float mnew = __builtin_fmaxf(mrow[qt], mx * qk_scale);
-        const float alpha = __builtin_amdgcn_exp2f(mrow[qt] - mnew);
-        mrow[qt] = mnew;
-#pragma unroll
-        for (int dt = 0; dt < C::NDT; ++dt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[dt][qt][r] *= alpha;
-        float ls = 0.0f;
-#pragma unroll
-        for (int kt = 0; kt < C::NKT; ++kt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][qt][r], qk_scale, -mnew));
-            sacc[kt][qt][r] = pv;
-            ls += pv;
-          }
-        lrow[qt] = lrow[qt] * alpha + ls;
-      }
-      // O^T += V^T P^T, one 16-key step at a time: the probabilities of a
-      // step are packed to the element type right before their MFMAs.
-#pragma unroll
-      for (int st = 0; st < C::PST; ++st) {
-        const int kt = st >> 1, ip = st & 1;
-        vec8 pf[C::NQT];
-#pragma unroll
-        for (int qt = 0; qt < C::NQT; ++qt) {
-          u32x4 pk;
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            pk[e] = pack2(E::from_f32(sacc[kt][qt][8 * ip + 2 * e]), E::from_f32(sacc[kt][qt][8 * ip + 2 * e + 1]));
-          pf[qt] = __builtin_bit_cast(vec8, pk);
-        }
-        const int ga = (C::KW * kh + 32 * kt + 16 * ip) / 4 + hl;
-#pragma unroll
-        for (int dt = 0; dt < C::NDT; ++dt) {
-          const int d = 32 * dt + l32;
-          const int sw = vswz(d, C::VGR);
-          const uint16_t* vrow = vd + d * BS;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + 4 * (ga ^ sw));
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 4 * ((ga + 2) ^ sw));
-          const vec8 va = __builtin_bit_cast(vec8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-#pragma unroll
-          for (int qt = 0; qt < C::NQT; ++qt) o[dt][qt] = E::mfma32(va, pf[qt], o[dt][qt]);
-        }
-      }
-    }
-    if (i + 1 < count) stash(stage ^ 1);
+    if (valid(cur)) compute(stage);
+    if (i + 1 < count) stash(Stage<ST ^ 1>{});
     __syncthreads();
     cur = nxt;
+  };
+
+  int cur = block_id(0);
+  fetch(valid(cur) ? cur : 0);
+  stash(Stage<0>{});
+  __syncthreads();
+  for (int i = 0; i < count; i += 2) {
+    step(Stage<0>{}, i, cur);
+    if (i + 1 < count) step(Stage<1>{}, i + 1, cur);
   }
 
-  // Merge the two key halves (waves kh = 0 and kh = 1 of the same qh).
-#pragma unroll
-  for (int qt = 0; qt < C::NQT; ++qt) lrow[qt] += __shfl_xor(lrow[qt], 32);
-  float* xo = reinterpret_cast<float*>(smem) + qh * (C::NDT * C::NQT * 16 * 64);
-  float* xm = reinterpret_cast<float*>(smem) + C::X_FLOATS + qh * (2 * C::NQT * 64);
+  // Merge the two key halves (waves kh = 0 and kh = 1 of the same qq).
+  lrow += __shfl_xor(lrow, 32);
+  float* xo = reinterpret_cast<float*>(smem) + qq * (C::NDT * 16 * 64);
+  float* xm = reinterpret_cast<float*>(smem) + C::X_FLOATS + qq * (2 * 64);
   if (kh == 1) {
 #pragma unroll
     for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
-      for (int qt = 0; qt < C::NQT; ++qt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) xo[((dt * C::NQT + qt) * 16 + r) * 64 + lane] = o[dt][qt][r];
-#pragma unroll
-    for (int qt = 0; qt < C::NQT; ++qt) {
-      xm[(2 * qt) * 64 + lane] = mrow[qt];
-      xm[(2 * qt + 1) * 64 + lane] = lrow[qt];
-    }
+      for (int r = 0; r < 16; ++r) xo[(dt * 16 + r) * 64 + lane] = o[dt][r];
+    xm[lane] = mrow;
+    xm[64 + lane] = lrow;
   }
   __syncthreads();
   if (kh == 0) {
+    const float m1 = xm[lane], l1 = xm[64 + lane];
+    const float mm = __builtin_fmaxf(mrow, m1);
+    const float a0 = __builtin_amdgcn_exp2f(mrow - mm), a1 = __builtin_amdgcn_exp2f(m1 - mm);
+    const float l = lrow * a0 + l1 * a1;
+    const float inv = 1.0f / l;
+    const int r = row0 + 32 * qq + l32;
+    if (r < a.Lq) {
+      uint16_t* orow = ohead + (int64_t)r * D;
 #pragma unroll
-    for (int qt = 0; qt < C::NQT; ++qt) {
-      const float m1 = xm[(2 * qt) * 64 + lane], l1 = xm[(2 * qt + 1) * 64 + lane];
-      const float mm = __builtin_fmaxf(mrow[qt], m1);
-      const float a0 = __builtin_amdgcn_exp2f(mrow[qt] - mm), a1 = __builtin_amdgcn_exp2f(m1 - mm);
-      const float l = lrow[qt] * a0 + l1 * a1;
-      const float inv = 1.0f / l;
-      const int r = row0 + C::QW * qh + 32 * qt + l32;
-      if (r < a.Lq) {
-        uint16_t* orow = ohead + (int64_t)r * D;
+      for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
-        for (int dt = 0; dt < C::NDT; ++dt)
+        for (int i4 = 0; i4 < 4; ++i4) {
+          float val[4];
 #pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) {
-            float val[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int rr = 4 * i4 + j;
-              const float o1 = xo[((dt * C::NQT + qt) * 16 + rr) * 64 + lane];
-              val[j] = (o[dt][qt][rr] * a0 + o1 * a1) * inv;
-            }
-            const u32x2 pk = {pack2(E::from_f32(val[0]), E::from_f32(val[1])),
-                              pack2(E::from_f32(val[2]), E::from_f32(val[3]))};
-            *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i4 + 4 * hl) = pk;
+          for (int j = 0; j < 4; ++j) {
+            const int rr = 4 * i4 + j;
+            const float o1 = xo[(dt * 16 + rr) * 64 + lane];
+            val[j] = (o[dt][rr] * a0 + o1 * a1) * inv;
           }
-        if (a.lse && hl == 0) a.lse[(int64_t)bh * a.Lq + r] = mm + __builtin_log2f(l);
-      }
+          const u32x2 pk = {cvt_pk<E>(val[0], val[1]), cvt_pk<E>(val[2], val[3])};
+          *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i4 + 4 * hl) = pk;
+        }
+      if (a.lse && hl == 0) a.lse[(int64_t)bh * a.Lq + r] = mm + __builtin_log2f(l);
     }
   }
 }

@@ -17,10 +17,15 @@
 // 3. the budget k follows the reference's integer arithmetic (int() truncation
 //    of a double product) and the remaining k - n_forced blocks are the
 //    largest non-forced scores, ties to the lower index: every key block gets
-//    the unique 32-bit key (order-preserving score bits << 16 | 0xFFFF - j) and
-//    a 32-step bitwise search finds the exact (k - n_forced)-th largest key;
+//    the unique 32-bit key (order-preserving score bits << 16 | 0xFFFF - j;
+//    0 marks a forced block) and a 32-step bitwise search finds the exact
+//    (k - n_forced)-th largest key;
 // 4. the selected blocks are written in ascending order by a ballot/prefix
 //    compaction over j, which replaces the reference's topk + sort.
+//
+// One wave per query row, WAVES rows per workgroup: every reduction is a
+// ballot + popcount inside the wave, so the kernel has no workgroup barrier.
+// The wave's keys live in its own LDS slice (4 bytes per key block).
 #include "li_common.hpp"
 
 namespace li {
@@ -44,16 +49,6 @@ __device__ __forceinline__ uint32_t order16(uint16_t bits) {
   return (bits & 0x8000u) ? (uint32_t)(~bits & 0xFFFFu) : (uint32_t)(bits | 0x8000u);
 }
 
-__device__ __forceinline__ int block_sum(int v, int* scratch) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  __syncthreads();
-  if (lane == 0) scratch[wave] = v;
-  __syncthreads();
-  return scratch[0] + scratch[1] + scratch[2] + scratch[3];
-}
-
 template <typename E, int D>
 __device__ __forceinline__ void load_row(const uint16_t* p, int64_t stride, bool vec, float* x) {
   if (vec) {
@@ -72,39 +67,48 @@ __device__ __forceinline__ void load_row(const uint16_t* p, int64_t stride, bool
   }
 }
 
+// Sequential fp32 sum of squares from +0.0, then the reference's normaliser
+// max(E(sqrt(.)), E(1e-12)).
 template <typename E, int D>
-__global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a) {
+__device__ __forceinline__ float norm_den(const float* x) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int d = 0; d < D; ++d) ss = ss + x[d] * x[d];
+  const float nrm = E::to_f32(E::from_f32(__builtin_sqrtf(ss)));
+  const float eps = E::to_f32(E::from_f32(1e-12f));
+  return nrm > eps ? nrm : eps;
+}
+
+__device__ __forceinline__ int wave_count(bool pred) { return __popcll(__ballot(pred)); }
+
+template <typename E, int D>
+__global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a, int waves) {
   extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
   const li_mask_params& p = a.p;
   const int nk = p.nk;
-  uint32_t* keys = smem;                                        // nk
-  uint8_t* forced = reinterpret_cast<uint8_t*>(smem + nk);       // nk
-  __shared__ float qv[D];
-  __shared__ float qden;
-  __shared__ int scratch[4];
-  __shared__ int wave_cnt[4];
-
-  const int qb = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int qb = blockIdx.x * waves + wave;
   const int bh = blockIdx.y;
+  if (qb >= p.nq) return;  // whole wave leaves; no workgroup barrier follows
   const int b = bh / a.NH, h = bh % a.NH;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool cosine = p.metric == LI_METRIC_COSINE;
+  uint32_t* keys = smem + (size_t)wave * (nk + D);
+  float* qv = reinterpret_cast<float*>(keys + nk);
 
-  // 1a. query pool row (normalised for cosine).
+  // 1a. query pool row, normalised for cosine (every lane computes the same
+  // sequential normaliser; lanes then own elements lane, lane + 64, ...).
   const uint16_t* qrow = a.qp + b * a.qs[0] + h * a.qs[1] + (int64_t)qb * a.qs[2];
-  if (tid < D) qv[tid] = E::to_f32(qrow[(int64_t)tid * a.qs[3]]);
-  __syncthreads();
+  for (int d = lane; d < D; d += 64) qv[d] = E::to_f32(qrow[(int64_t)d * a.qs[3]]);
+  __builtin_amdgcn_wave_barrier();
   if (cosine) {
-    if (tid == 0) {
-      float ss = 0.0f;
-      for (int d = 0; d < D; ++d) ss = ss + qv[d] * qv[d];
-      const float nrm = E::to_f32(E::from_f32(__builtin_sqrtf(ss)));
-      const float eps = E::to_f32(E::from_f32(1e-12f));
-      qden = nrm > eps ? nrm : eps;
-    }
-    __syncthreads();
-    if (tid < D) qv[tid] = E::to_f32(E::from_f32(qv[tid] / qden));
-    __syncthreads();
+    float ss = 0.0f;
+    for (int d = 0; d < D; ++d) ss = ss + qv[d] * qv[d];
+    const float nrm = E::to_f32(E::from_f32(__builtin_sqrtf(ss)));
+    const float eps = E::to_f32(E::from_f32(1e-12f));
+    const float den = nrm > eps ? nrm : eps;
+    __builtin_amdgcn_wave_barrier();
+    for (int d = lane; d < D; d += 64) qv[d] = E::to_f32(E::from_f32(qv[d] / den));
+    __builtin_amdgcn_wave_barrier();
   }
 
   // 1b/2. scores, forced flags, order keys.
@@ -115,41 +119,37 @@ __global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a) {
                    a.ks[1] % 8 == 0 && a.ks[2] % 8 == 0;
   const uint16_t* kbase = a.kp + b * a.ks[0] + h * a.ks[1];
   uint16_t* srow = a.scores ? a.scores + ((int64_t)bh * p.nq + qb) * nk : nullptr;
-  int nf_local = 0;
-  for (int j = tid; j < nk; j += 256) {
-    float x[D];
-    load_row<E, D>(kbase + (int64_t)j * a.ks[2], a.ks[3], vec, x);
-    float dot = 0.0f;
-    if (cosine) {
-      float ss = 0.0f;
+  int nf = 0;
+  for (int j0 = 0; j0 < nk; j0 += 64) {
+    const int j = j0 + lane;
+    bool f = false;
+    if (j < nk) {
+      float x[D];
+      load_row<E, D>(kbase + (int64_t)j * a.ks[2], a.ks[3], vec, x);
+      float dot = 0.0f;
+      if (cosine) {
+        const float den = norm_den<E, D>(x);
 #pragma unroll
-      for (int d = 0; d < D; ++d) ss = ss + x[d] * x[d];
-      const float nrm = E::to_f32(E::from_f32(__builtin_sqrtf(ss)));
-      const float eps = E::to_f32(E::from_f32(1e-12f));
-      const float den = nrm > eps ? nrm : eps;
+        for (int d = 0; d < D; ++d) dot = dot + qv[d] * E::to_f32(E::from_f32(x[d] / den));
+      } else {
 #pragma unroll
-      for (int d = 0; d < D; ++d) dot = dot + qv[d] * E::to_f32(E::from_f32(x[d] / den));
-    } else {
-#pragma unroll
-      for (int d = 0; d < D; ++d) dot = dot + qv[d] * x[d];
+        for (int d = 0; d < D; ++d) dot = dot + qv[d] * x[d];
+      }
+      uint16_t s = E::from_f32(dot);
+      if (p.metric == LI_METRIC_SCALED_DOT) s = E::from_f32(E::to_f32(s) * p.scale);
+      if (srow) srow[j] = s;
+      f = (p.n_recent > 0) && (j >= nk - p.n_recent);
+      if (p.force_diag && j == pos) f = true;
+      if (p.force_sink && j == qb % hw) f = true;
+      if (p.force_neighbors && pos >= 0 && pos < nk) {
+        const int jt = j / hw, jh = (j % hw) / p.nw, jw = j % p.nw;
+        if (abs(jt - pt) + abs(jh - ph) + abs(jw - pw) <= 1) f = true;
+      }
+      keys[j] = f ? 0u : ((order16(s) << 16) | (0xFFFFu - (uint32_t)j));
     }
-    uint16_t s = E::from_f32(dot);
-    if (p.metric == LI_METRIC_SCALED_DOT) s = E::from_f32(E::to_f32(s) * p.scale);
-    if (srow) srow[j] = s;
-
-    bool f = (p.n_recent > 0) && (j >= nk - p.n_recent);
-    if (p.force_diag && j == pos) f = true;
-    if (p.force_sink && j == qb % hw) f = true;
-    if (p.force_neighbors && pos >= 0 && pos < nk) {
-      const int jt = j / hw, jh = (j % hw) / p.nw, jw = j % p.nw;
-      const int dist = abs(jt - pt) + abs(jh - ph) + abs(jw - pw);
-      if (dist <= 1) f = true;
-    }
-    forced[j] = f ? 1 : 0;
-    keys[j] = f ? 0u : ((order16(s) << 16) | (0xFFFFu - (uint32_t)j));
-    nf_local += f ? 1 : 0;
+    nf += wave_count(f);
   }
-  const int nf = block_sum(nf_local, scratch);  // also orders the LDS writes above
+  __builtin_amdgcn_wave_barrier();
 
   // 3. budget.
   int k;
@@ -169,18 +169,21 @@ __global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a) {
     k = k > nk ? nk : k;
     k = k < nf ? nf : k;
   }
-  const int kk = k - nf;       // non-forced blocks to keep
+  const int kk = k - nf;  // non-forced blocks to keep
   const int nfree = nk - nf;
 
-  // Exact kk-th largest key among non-forced blocks.
-  uint32_t thr = 0;
+  // Exact kk-th largest key among non-forced blocks (forced keys are 0 and
+  // never reach a candidate, which is always >= 1 here).
+  uint32_t thr = 1u;
   if (kk > 0 && kk < nfree) {
     uint32_t prefix = 0;
     for (int bit = 31; bit >= 0; --bit) {
       const uint32_t cand = prefix | (1u << bit);
       int c = 0;
-      for (int j = tid; j < nk; j += 256) c += (!forced[j] && keys[j] >= cand) ? 1 : 0;
-      c = block_sum(c, scratch);
+      for (int j0 = 0; j0 < nk; j0 += 64) {
+        const int j = j0 + lane;
+        c += wave_count(j < nk && keys[j] >= cand);
+      }
       if (c >= kk) prefix = cand;
     }
     thr = prefix;
@@ -190,25 +193,22 @@ __global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a) {
   const int64_t row = (int64_t)bh * p.nq + qb;
   int32_t* irow = a.indices + row * p.kmax;
   const int ntxt = p.num_txt_blk;
-  for (int i = tid; i < ntxt && i < p.kmax; i += 256) irow[i] = i;
-  int base = 0;
-  for (int c0 = 0; c0 < nk; c0 += 256) {
-    const int j = c0 + tid;
+  for (int i = lane; i < ntxt && i < p.kmax; i += 64) irow[i] = i;
+  int base = ntxt;
+  for (int j0 = 0; j0 < nk; j0 += 64) {
+    const int j = j0 + lane;
     bool sel = false;
-    if (j < nk) sel = forced[j] || (kk > 0 && (kk >= nfree || keys[j] >= thr));
+    if (j < nk) {
+      const uint32_t key = keys[j];
+      sel = key == 0u || (kk > 0 && key >= thr);
+    }
     const uint64_t m = __ballot(sel);
-    const int lp = __popcll(m & ((1ull << lane) - 1ull));
-    if (lane == 0) wave_cnt[wave] = __popcll(m);
-    __syncthreads();
-    int off = base;
-    for (int w = 0; w < wave; ++w) off += wave_cnt[w];
-    const int dst = ntxt + off + lp;
+    const int dst = base + __popcll(m & ((1ull << lane) - 1ull));
     if (sel && dst < p.kmax) irow[dst] = j + ntxt;
-    base += wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
-    __syncthreads();
+    base += __popcll(m);
   }
-  for (int i = ntxt + k + tid; i < p.kmax; i += 256) irow[i] = 0;
-  if (tid == 0) a.counts[row] = ntxt + k;
+  for (int i = ntxt + k + lane; i < p.kmax; i += 64) irow[i] = 0;
+  if (lane == 0) a.counts[row] = ntxt + k;
 }
 
 }  // namespace
@@ -245,18 +245,23 @@ extern "C" int li_block_mask(int dtype, int32_t B, int32_t NH, int32_t D, const 
   a.counts = counts;
   a.scores = static_cast<uint16_t*>(scores);
   a.NH = NH;
-  const size_t lds = (size_t)p.nk * 4 + (size_t)p.nk + 16;
-  dim3 grid((unsigned)p.nq, (unsigned)(B * NH));
+  // Per-wave LDS slice: nk keys + the query row; up to 4 waves (rows) per workgroup.
+  const size_t per_wave = ((size_t)p.nk + D) * 4;
+  int waves = (int)(65536 / per_wave);
+  waves = waves < 1 ? 1 : (waves > 4 ? 4 : waves);
+  const size_t lds = per_wave * waves;
+  dim3 grid((unsigned)((p.nq + waves - 1) / waves), (unsigned)(B * NH));
+  dim3 block((unsigned)(64 * waves));
   hipStream_t s = static_cast<hipStream_t>(stream);
   clear_launch_error();
   if (dtype == LI_DTYPE_BF16 && D == 128)
-    hipLaunchKernelGGL((block_mask_kernel<Bf16, 128>), grid, dim3(256), lds, s, a);
+    hipLaunchKernelGGL((block_mask_kernel<Bf16, 128>), grid, block, lds, s, a, waves);
   else if (dtype == LI_DTYPE_BF16 && D == 64)
-    hipLaunchKernelGGL((block_mask_kernel<Bf16, 64>), grid, dim3(256), lds, s, a);
+    hipLaunchKernelGGL((block_mask_kernel<Bf16, 64>), grid, block, lds, s, a, waves);
   else if (dtype == LI_DTYPE_F16 && D == 128)
-    hipLaunchKernelGGL((block_mask_kernel<F16, 128>), grid, dim3(256), lds, s, a);
+    hipLaunchKernelGGL((block_mask_kernel<F16, 128>), grid, block, lds, s, a, waves);
   else if (dtype == LI_DTYPE_F16 && D == 64)
-    hipLaunchKernelGGL((block_mask_kernel<F16, 64>), grid, dim3(256), lds, s, a);
+    hipLaunchKernelGGL((block_mask_kernel<F16, 64>), grid, block, lds, s, a, waves);
   else
     return LI_ERR_UNSUPPORTED;
   return launch_status();
