@@ -185,29 +185,40 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_kernel(BsaArgs a) {
 
   u32x4 kst[C::IT];
   u32x4 vst[C::IT];
-  auto fetch = [&](int blk) {
+  auto fetch_k = [&](int blk) {
     const uint16_t* kb = khead + (int64_t)blk * BS * D;
+#pragma unroll
+    for (int it = 0; it < C::IT; ++it) {
+      const int u = tid + C::NTHR * it;
+      if (C::UNITS % C::NTHR == 0 || u < C::UNITS)
+        kst[it] = *reinterpret_cast<const u32x4*>(kb + (u / C::KGR) * D + 8 * (u % C::KGR));
+    }
+  };
+  auto fetch_v = [&](int blk) {
     const uint16_t* vb = vhead + (int64_t)blk * BS * D;
 #pragma unroll
     for (int it = 0; it < C::IT; ++it) {
       const int u = tid + C::NTHR * it;
-      if (C::UNITS % C::NTHR == 0 || u < C::UNITS) {
-        kst[it] = *reinterpret_cast<const u32x4*>(kb + (u / C::KGR) * D + 8 * (u % C::KGR));
+      if (C::UNITS % C::NTHR == 0 || u < C::UNITS)
         vst[it] = *reinterpret_cast<const u32x4*>(vb + (u / C::KGR) * D + 8 * (u % C::KGR));
-      }
     }
   };
-  auto stash = [&](auto stage) {
-    constexpr int ST = decltype(stage)::value;
-    uint16_t* kd = kbuf + ST * C::K_STAGE;
-    uint16_t* vd = vbuf + ST * C::V_STAGE;
+  auto stash_k = [&](auto stage) {
+    uint16_t* kd = kbuf + decltype(stage)::value * C::K_STAGE;
 #pragma unroll
     for (int it = 0; it < C::IT; ++it) {
       const int u = tid + C::NTHR * it;
-      if (C::UNITS % C::NTHR == 0 || u < C::UNITS) {
+      if (C::UNITS % C::NTHR == 0 || u < C::UNITS)
         *reinterpret_cast<u32x4*>(kd + (u / C::KGR) * C::KP + 8 * (u % C::KGR)) = kst[it];
+    }
+  };
+  auto stash_v = [&](auto stage) {
+    uint16_t* vd = vbuf + decltype(stage)::value * C::V_STAGE;
+#pragma unroll
+    for (int it = 0; it < C::IT; ++it) {
+      const int u = tid + C::NTHR * it;
+      if (C::UNITS % C::NTHR == 0 || u < C::UNITS)
         *reinterpret_cast<u32x4*>(vd + (u / C::KGR) * C::VP + 8 * (u % C::KGR)) = vst[it];
-      }
     }
   };
 
@@ -219,12 +230,9 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_kernel(BsaArgs a) {
   float mrow = -__builtin_inff(), lrow = 0.0f;
   const float qk_scale = a.qk_scale;
 
-  auto compute = [&](auto stage) {
-    constexpr int ST = decltype(stage)::value;
-    const uint16_t* kd = kbuf + ST * C::K_STAGE;
-    const uint16_t* vd = vbuf + ST * C::V_STAGE;
-    // S^T = K Q^T for this wave's key half.
-    f32x16 sacc[C::NKT];
+  // S^T = K Q^T of one block for this wave's key half.
+  auto scores = [&](auto stage, f32x16* sacc) {
+    const uint16_t* kd = kbuf + decltype(stage)::value * C::K_STAGE;
 #pragma unroll
     for (int kt = 0; kt < C::NKT; ++kt)
 #pragma unroll
@@ -237,14 +245,19 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_kernel(BsaArgs a) {
         sacc[kt] = E::mfma32(ka, qf[s], sacc[kt]);
       }
     }
-    // Online softmax: lane owns query column l32; the other half of the
-    // wave's keys for that query sits in lane ^ 32.
+  };
+  // Online softmax of one block, in two parts so that the next block's score
+  // MFMAs can be issued between them (same basic block as the exponentials).
+  // The lane owns query column l32; the other half of the wave's keys for
+  // that query sits in lane ^ 32, reached with v_permlane32_swap.
+  auto softmax_max = [&](f32x16* sacc) {
     float mx = sacc[0][0];
 #pragma unroll
     for (int kt = 0; kt < C::NKT; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, sacc[kt][r]);
-    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32)) * qk_scale;
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    mx = __builtin_fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * qk_scale;
     if (__ballot(mx > mrow + 8.0f)) {
       const float mnew = __builtin_fmaxf(mrow, mx);
       const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
@@ -255,17 +268,25 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_kernel(BsaArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
     }
+  };
+  // Probabilities overwrite the scores.  mrow is still -inf only when every
+  // block so far was skipped (all scores -inf): the offset 0 keeps exp2 at 0.
+  auto softmax_exp = [&](f32x16* sacc) {
+    const float moff = mrow == -__builtin_inff() ? 0.0f : mrow;
     float ls = 0.0f;
 #pragma unroll
     for (int kt = 0; kt < C::NKT; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][r], qk_scale, -mrow));
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][r], qk_scale, -moff));
         sacc[kt][r] = pv;
         ls += pv;
       }
     lrow += ls;
-    // O^T += V^T P^T, one 16-key step at a time.
+  };
+  // O^T += V^T P^T, one 16-key step at a time.
+  auto pv_update = [&](auto stage, f32x16* sacc) {
+    const uint16_t* vd = vbuf + decltype(stage)::value * C::V_STAGE;
 #pragma unroll
     for (int st = 0; st < C::PST; ++st) {
       const int kt = st >> 1, ip = st & 1;
@@ -286,29 +307,58 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_kernel(BsaArgs a) {
 
   auto block_id = [&](int i) { return __builtin_amdgcn_readfirstlane(irow[(int64_t)i * a.is[3]]); };
   auto valid = [&](int id_) { return (unsigned)id_ < (unsigned)a.nkb; };
+  auto safe = [&](int id_) { return valid(id_) ? id_ : 0; };
 
-  // One block per step: prefetch the next block into registers, compute the
-  // current stage, then write the prefetched block to the other stage.
-  auto step = [&](auto stage, int i, int& cur) {
+  // Software pipeline, one kept block per step i (K runs one block ahead of V):
+  //   fetch K(i+2), V(i+1) into registers;
+  //   row max of S(i) (and a rare rescale), then S(i+1) = K(i+1) Q^T on the
+  //   MFMA pipe interleaved with the exponentials of S(i) on the VALU;
+  //   O += V(i)^T P(i);
+  //   write K(i+2) into K's stage i%2 and V(i+1) into V's stage (i+1)%2; barrier.
+  // Stage i%2 of K held K(i), last read in step i-1 (hence the barrier after
+  // the prologue's S(0)); V's stage (i+1)%2 held V(i-1), last read in step i-1.
+  // The step has no branch besides the rescale test: past the last block the
+  // prefetch repeats the last block (indices stay in range) and S(i+1) is
+  // computed on a stale stage and never used.  A block id out of range is
+  // loaded as block 0 and skipped through -inf scores.
+  f32x16 sa[C::NKT], sb[C::NKT];
+  const int id0 = block_id(0);
+  const int id1 = block_id(count > 1 ? 1 : 0);
+  fetch_k(safe(id0));
+  fetch_v(safe(id0));
+  stash_k(Stage<0>{});
+  stash_v(Stage<0>{});
+  fetch_k(safe(id1));
+  stash_k(Stage<1>{});
+  __syncthreads();
+  scores(Stage<0>{}, sa);
+  __syncthreads();
+
+  auto step = [&](auto stage, int i, int& cur, int& nxt, f32x16* s_cur, f32x16* s_nxt) {
     constexpr int ST = decltype(stage)::value;
-    int nxt = 0;
-    if (i + 1 < count) {
-      nxt = block_id(i + 1);
-      fetch(valid(nxt) ? nxt : 0);
+    const int nn = block_id(i + 2 < count ? i + 2 : count - 1);
+    fetch_k(safe(nn));
+    fetch_v(safe(nxt));
+    if (!valid(cur)) {
+#pragma unroll
+      for (int kt = 0; kt < C::NKT; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s_cur[kt][r] = -__builtin_inff();
     }
-    if (valid(cur)) compute(stage);
-    if (i + 1 < count) stash(Stage<ST ^ 1>{});
+    softmax_max(s_cur);
+    scores(Stage<ST ^ 1>{}, s_nxt);
+    softmax_exp(s_cur);
+    pv_update(stage, s_cur);
+    stash_k(stage);
+    stash_v(Stage<ST ^ 1>{});
     __syncthreads();
     cur = nxt;
+    nxt = nn;
   };
-
-  int cur = block_id(0);
-  fetch(valid(cur) ? cur : 0);
-  stash(Stage<0>{});
-  __syncthreads();
+  int cur = id0, nxt = id1;
   for (int i = 0; i < count; i += 2) {
-    step(Stage<0>{}, i, cur);
-    if (i + 1 < count) step(Stage<1>{}, i + 1, cur);
+    step(Stage<0>{}, i, cur, nxt, sa, sb);
+    if (i + 1 < count) step(Stage<1>{}, i + 1, cur, nxt, sb, sa);
   }
 
   // Merge the two key halves (waves kh = 0 and kh = 1 of the same qq).
@@ -352,6 +402,267 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_kernel(BsaArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// D = 128 variant with direct-to-LDS block loads (global_load_lds_dwordx4).
+//
+// Each wave-wide DMA instruction writes 1 KiB of LDS at consecutive 16-byte
+// slots, one per lane; the layout is chosen through each lane's global
+// address:
+//  * K stage: 4-row chunks of 1 KiB at a 1088-byte pitch; row r of a chunk
+//    at +256 r, its 16-byte granule g at slot g ^ r.  The b128 operand reads
+//    of 16 rows kperm(i) then hit 16 distinct bank windows, and a lane's
+//    address for MFMA step s is one of two per-lane bases plus 64*(s/2).
+//  * V stage: 256-byte rows; the 64-byte granule q of row r at q ^ (r % 4).
+//    Each transposing read covers 4 consecutive rows, which then occupy the
+//    4 distinct 64-byte bank windows.
+// Block i+1 is loaded into the other stage while block i is computed; the
+// barrier at the end of a step (which waits for all of the wave's loads)
+// publishes it.  No staging registers, no LDS store instructions.
+template <int BS>
+struct DmaCfg {
+  static constexpr int D = 128;
+  static constexpr int WAVES = 2 * (BS / 32);
+  static constexpr int NTHR = 64 * WAVES;
+  static constexpr int KW = BS / 2;
+  static constexpr int NKT = KW / 32;
+  static constexpr int DS = D / 16;
+  static constexpr int NDT = D / 32;
+  static constexpr int PST = KW / 16;
+  static constexpr int CHUNKS = BS / 4;                // 1 KiB chunks per K (or V) block
+  static constexpr int CPW = CHUNKS / WAVES;           // chunks per wave
+  static constexpr int K_STAGE_BYTES = CHUNKS * 1088;
+  static constexpr int V_STAGE_BYTES = BS * 256;
+  static constexpr int NQW = WAVES / 2;
+};
+
+template <typename E, int BS>
+__global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
+  using C = DmaCfg<BS>;
+  constexpr int D = 128;
+  typedef typename E::vec8 vec8;
+  typedef __attribute__((address_space(3))) void lds_void;
+  // Separate arrays per stage let the compiler see that a load into one stage
+  // never aliases the reads of the other.
+  __shared__ __attribute__((aligned(16))) char ks0[C::K_STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char ks1[C::K_STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char vs0[C::V_STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char vs1[C::V_STAGE_BYTES];
+  static_assert(C::NQW / 2 * C::NDT * 16 * 64 * 4 <= C::K_STAGE_BYTES, "epilogue exchange must fit a K stage");
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int qq = wave >> 1, kh = wave & 1;
+  const int l32 = lane & 31, hl = lane >> 5;
+
+  const int nwg = gridDim.x, id = blockIdx.x;
+  const int xcd = id & 7, slot = id >> 3;
+  const int per = nwg >> 3, rem = nwg & 7;
+  const int w = xcd * per + (xcd < rem ? xcd : rem) + slot;
+  const int bh = w / a.nqt, m = w % a.nqt;
+  const int b = bh / a.NH, h = bh % a.NH;
+
+  const uint16_t* qhead = a.q + (int64_t)bh * a.Lq * D;
+  const uint16_t* khead = a.k + (int64_t)bh * a.nkb * BS * D;
+  const uint16_t* vhead = a.v + (int64_t)bh * a.nkb * BS * D;
+  uint16_t* ohead = a.out + (int64_t)bh * a.Lq * D;
+  const int32_t* irow = a.idx + b * a.is[0] + h * a.is[1] + (int64_t)m * a.is[2];
+  int count = a.cnt[b * a.cs[0] + h * a.cs[1] + (int64_t)m * a.cs[2]];
+  count = count < 0 ? 0 : (count > a.n_cols ? a.n_cols : count);
+  count = __builtin_amdgcn_readfirstlane(count);
+  const int row0 = m * BS;
+
+  if (count == 0) {
+    for (int u = tid; u < BS * (D / 8); u += C::NTHR) {
+      const int r = row0 + u / (D / 8);
+      if (r < a.Lq) *reinterpret_cast<u32x4*>(ohead + (int64_t)r * D + 8 * (u % (D / 8))) = u32x4{0u, 0u, 0u, 0u};
+    }
+    if (a.lse)
+      for (int r = tid; r < BS; r += C::NTHR)
+        if (row0 + r < a.Lq) a.lse[(int64_t)bh * a.Lq + row0 + r] = -__builtin_inff();
+    return;
+  }
+
+  vec8 qf[C::DS];
+  {
+    const int r = row0 + 32 * qq + l32;
+#pragma unroll
+    for (int s = 0; s < C::DS; ++s) {
+      u32x4 x = {0u, 0u, 0u, 0u};
+      if (r < a.Lq) x = *reinterpret_cast<const u32x4*>(qhead + (int64_t)r * D + 16 * s + 8 * hl);
+      qf[s] = __builtin_bit_cast(vec8, x);
+    }
+  }
+
+  // DMA source byte offsets of this lane within a chunk; the chunk base is
+  // wave-uniform (scalar registers), so each load is base + constant lane
+  // offset with no per-load vector address arithmetic.
+  const int rp = lane >> 4;
+  const uint32_t k_src = 2u * (rp * D + 8 * ((lane & 15) ^ rp));
+  const uint32_t v_src = 2u * (rp * D + 32 * (((lane & 15) >> 2) ^ rp) + 8 * (lane & 3));
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  auto load_block = [&](int blk, char* kd, char* vd) {
+    const char* kb = reinterpret_cast<const char*>(khead + (int64_t)blk * BS * D);
+    const char* vb = reinterpret_cast<const char*>(vhead + (int64_t)blk * BS * D);
+#pragma unroll
+    for (int j = 0; j < C::CPW; ++j) {
+      const int c = wave_s * C::CPW + j;
+      __builtin_amdgcn_global_load_lds(kb + 8 * c * D + k_src, (lds_void*)(kd + c * 1088), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vb + 8 * c * D + v_src, (lds_void*)(vd + c * 1024), 16, 0, 0);
+    }
+  };
+
+  // K operand byte offsets: row R = KW*kh + kperm(l32) (+32 kt), granule 2s+hl.
+  const int R = C::KW * kh + kperm(l32);
+  const int rc = R & 3;
+  const int k_base = (R >> 2) * 1088 + rc * 256 + 16 * (hl ^ (rc & 1));
+  const int k_off[2] = {k_base + 32 * (rc >> 1), k_base + 32 * (1 ^ (rc >> 1))};
+  // V^T operand byte offsets for the transposing reads, one per 32-wide d tile.
+  const int t16 = lane & 15, g16 = lane >> 4;
+  const int v_base = (C::KW * kh + 8 * hl + (t16 >> 2)) * 256 + 32 * (g16 & 1) + 8 * (t16 & 3);
+  int v_off[C::NDT];
+#pragma unroll
+  for (int dt = 0; dt < C::NDT; ++dt) v_off[dt] = v_base + 64 * (dt ^ (t16 >> 2));
+
+  f32x16 o[C::NDT];
+#pragma unroll
+  for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[dt][r] = 0.0f;
+  float mrow = -__builtin_inff(), lrow = 0.0f;
+  const float qk_scale = a.qk_scale;
+
+  auto compute = [&](const char* kd, const char* vd) {
+    f32x16 sacc[C::NKT];
+#pragma unroll
+    for (int kt = 0; kt < C::NKT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < C::DS; ++s) {
+#pragma unroll
+      for (int kt = 0; kt < C::NKT; ++kt) {
+        const vec8 ka = __builtin_bit_cast(
+            vec8, *reinterpret_cast<const u32x4*>(kd + k_off[s & 1] + 8704 * kt + 64 * (s >> 1)));
+        sacc[kt] = E::mfma32(ka, qf[s], sacc[kt]);
+      }
+    }
+    float mx = sacc[0][0];
+#pragma unroll
+    for (int kt = 0; kt < C::NKT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, sacc[kt][r]);
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    mx = __builtin_fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * qk_scale;
+    if (__ballot(mx > mrow + 8.0f)) {
+      const float mnew = __builtin_fmaxf(mrow, mx);
+      const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+      mrow = mnew;
+      lrow *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    }
+    float ls = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < C::NKT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][r], qk_scale, -mrow));
+        sacc[kt][r] = pv;
+        ls += pv;
+      }
+    lrow += ls;
+#pragma unroll
+    for (int st = 0; st < C::PST; ++st) {
+      const int kt = st >> 1, ip = st & 1;
+      u32x4 pk;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pk[e] = cvt_pk<E>(sacc[kt][8 * ip + 2 * e], sacc[kt][8 * ip + 2 * e + 1]);
+      const vec8 pf = __builtin_bit_cast(vec8, pk);
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt) {
+        const uint16_t* pv = reinterpret_cast<const uint16_t*>(vd + v_off[dt] + (32 * kt + 16 * ip) * 256);
+        const u32x2 lo = lds_read_tr(pv);
+        const u32x2 hi = lds_read_tr(pv + 4 * 128);
+        o[dt] = E::mfma32(__builtin_bit_cast(vec8, u32x4{lo[0], lo[1], hi[0], hi[1]}), pf, o[dt]);
+      }
+    }
+  };
+
+  // Block ids are wave-uniform: read them through the scalar cache.
+  typedef __attribute__((address_space(4))) const int32_t const_i32;
+  const_i32* irow_s = (const_i32*)irow;
+  auto block_id = [&](int i) { return irow_s[(int64_t)i * a.is[3]]; };
+  auto valid = [&](int id_) { return (unsigned)id_ < (unsigned)a.nkb; };
+
+  // Step i: load block i+1 into the other stage, compute block i (skipped,
+  // by a uniform branch, when its id is out of range), barrier.  The other
+  // stage held block i-1, last read before the previous barrier.
+  int cur = block_id(0);
+  load_block(valid(cur) ? cur : 0, ks0, vs0);
+  int nxt = block_id(count > 1 ? 1 : 0);
+  __syncthreads();
+  auto step = [&](char* kc, char* vc, char* kn, char* vn, int i) {
+    const int nn = block_id(i + 2 < count ? i + 2 : count - 1);
+    if (i + 1 < count) load_block(valid(nxt) ? nxt : 0, kn, vn);
+    if (valid(cur)) compute(kc, vc);
+    __syncthreads();
+    cur = nxt;
+    nxt = nn;
+  };
+  for (int i = 0; i < count; i += 2) {
+    step(ks0, vs0, ks1, vs1, i);
+    if (i + 1 < count) step(ks1, vs1, ks0, vs0, i + 1);
+  }
+
+  // Merge the two key halves (waves kh = 0 and kh = 1 of the same qq).
+  lrow += __shfl_xor(lrow, 32);
+  float* xo = reinterpret_cast<float*>(qq < C::NQW / 2 || C::NQW == 1 ? ks0 : ks1) +
+              (qq % (C::NQW > 1 ? C::NQW / 2 : 1)) * (C::NDT * 16 * 64);
+  float* xm = reinterpret_cast<float*>(vs0) + qq * (2 * 64);
+  if (kh == 1) {
+#pragma unroll
+    for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xo[(dt * 16 + r) * 64 + lane] = o[dt][r];
+    xm[lane] = mrow;
+    xm[64 + lane] = lrow;
+  }
+  __syncthreads();
+  if (kh == 0) {
+    const float m1 = xm[lane], l1 = xm[64 + lane];
+    const float mm = __builtin_fmaxf(mrow, m1);
+    const float a0 = __builtin_amdgcn_exp2f(mrow - mm), a1 = __builtin_amdgcn_exp2f(m1 - mm);
+    const float l = lrow * a0 + l1 * a1;
+    const float inv = 1.0f / l;
+    const int r = row0 + 32 * qq + l32;
+    if (r < a.Lq) {
+      uint16_t* orow = ohead + (int64_t)r * D;
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+          float val[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int rr = 4 * i4 + j;
+            val[j] = (o[dt][rr] * a0 + xo[(dt * 16 + rr) * 64 + lane] * a1) * inv;
+          }
+          const u32x2 pk = {cvt_pk<E>(val[0], val[1]), cvt_pk<E>(val[2], val[3])};
+          *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i4 + 4 * hl) = pk;
+        }
+      if (a.lse && hl == 0) a.lse[(int64_t)bh * a.Lq + r] = mm + __builtin_log2f(l);
+    }
+  }
+}
+
+template <typename E, int BS>
+int launch_bsa_dma(BsaArgs& a, int tiles, hipStream_t s) {
+  clear_launch_error();
+  hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, BS>), dim3(tiles), dim3(DmaCfg<BS>::NTHR), 0, s, a);
+  return launch_status();
+}
+
 template <typename E, int BS, int D>
 int launch_bsa(BsaArgs& a, int tiles, hipStream_t s) {
   clear_launch_error();
@@ -361,9 +672,9 @@ int launch_bsa(BsaArgs& a, int tiles, hipStream_t s) {
 
 template <typename E>
 int dispatch_bsa(BsaArgs& a, int bs, int D, int tiles, hipStream_t s) {
-  if (bs == 128 && D == 128) return launch_bsa<E, 128, 128>(a, tiles, s);
+  if (bs == 128 && D == 128) return launch_bsa_dma<E, 128>(a, tiles, s);
   if (bs == 128 && D == 64) return launch_bsa<E, 128, 64>(a, tiles, s);
-  if (bs == 64 && D == 128) return launch_bsa<E, 64, 128>(a, tiles, s);
+  if (bs == 64 && D == 128) return launch_bsa_dma<E, 64>(a, tiles, s);
   if (bs == 64 && D == 64) return launch_bsa<E, 64, 64>(a, tiles, s);
   return LI_ERR_UNSUPPORTED;
 }
