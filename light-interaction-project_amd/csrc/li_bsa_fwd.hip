@@ -435,6 +435,46 @@ struct DmaCfg {
   static constexpr int NQW = WAVES / 2;
 };
 
+// 16 bytes per lane from global memory (wave-uniform base in SGPRs plus a
+// per-lane byte offset) straight into LDS at lds_addr + 16 * lane
+// (global_load_lds_dwordx4).  Issued as inline assembly so that the
+// compiler's wait-count bookkeeping does not see it: the compiler would
+// otherwise treat every pending LDS DMA as making the LDS counter unordered
+// and drain all operand reads in flight (lgkmcnt(0)) after each one.  Being
+// invisible only makes the compiler's own waits stricter (the extra loads
+// are counted by the hardware), never weaker; the caller publishes the data
+// with wait_vm0() before a barrier.  The s_nop covers the M0-write to LDS-DMA
+// hazard.
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_addr) : "memory");
+}
+__device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Scheduling pins of an M phase (one basic block): the operand reads of the
+// first LA MFMAs, then per MFMA u: the MFMA, the reads of MFMA u + LA (two
+// transposing reads for a P V step, one 16-byte read for an S step) and, when
+// the phase loads a stage, one DMA after every odd MFMA.
+template <int NPV, int U, int END>
+__device__ __forceinline__ void sched_first_reads() {
+  if constexpr (U < END) {
+    __builtin_amdgcn_sched_group_barrier(0x100, U < NPV ? 2 : 1, 0);
+    sched_first_reads<NPV, U + 1, END>();
+  }
+}
+template <int NPV, int NU, int LA, bool LOADS, int U>
+__device__ __forceinline__ void sched_m_units() {
+  if constexpr (U < NU) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if constexpr (U + LA < NU) __builtin_amdgcn_sched_group_barrier(0x100, U + LA < NPV ? 2 : 1, 0);
+    sched_m_units<NPV, NU, LA, LOADS, U + 1>();
+  }
+}
+template <int NPV, int NU, int LA, bool LOADS>
+__device__ __forceinline__ void sched_m_phase() {
+  sched_first_reads<NPV, 0, LA>();
+  sched_m_units<NPV, NU, LA, LOADS, 0>();
+}
+
 template <typename E, int BS>
 __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   using C = DmaCfg<BS>;
@@ -499,16 +539,6 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   const uint32_t k_src = 2u * (rp * D + 8 * ((lane & 15) ^ rp));
   const uint32_t v_src = 2u * (rp * D + 32 * (((lane & 15) >> 2) ^ rp) + 8 * (lane & 3));
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-  auto load_block = [&](int blk, char* kd, char* vd) {
-    const char* kb = reinterpret_cast<const char*>(khead + (int64_t)blk * BS * D);
-    const char* vb = reinterpret_cast<const char*>(vhead + (int64_t)blk * BS * D);
-#pragma unroll
-    for (int j = 0; j < C::CPW; ++j) {
-      const int c = wave_s * C::CPW + j;
-      __builtin_amdgcn_global_load_lds(kb + 8 * c * D + k_src, (lds_void*)(kd + c * 1088), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vb + 8 * c * D + v_src, (lds_void*)(vd + c * 1024), 16, 0, 0);
-    }
-  };
 
   // K operand byte offsets: row R = KW*kh + kperm(l32) (+32 kt), granule 2s+hl.
   const int R = C::KW * kh + kperm(l32);
@@ -530,21 +560,26 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   float mrow = -__builtin_inff(), lrow = 0.0f;
   const float qk_scale = a.qk_scale;
 
-  auto compute = [&](const char* kd, const char* vd) {
-    f32x16 sacc[C::NKT];
+  // Score tile S^T = K Q^T of one block (this wave's key half).
+  f32x16 sacc[C::NKT];
+  auto scores = [&](const char* kd) {
+    f32x16 z;
 #pragma unroll
-    for (int kt = 0; kt < C::NKT; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[kt][r] = 0.0f;
+    for (int r = 0; r < 16; ++r) z[r] = 0.0f;
 #pragma unroll
     for (int s = 0; s < C::DS; ++s) {
 #pragma unroll
       for (int kt = 0; kt < C::NKT; ++kt) {
         const vec8 ka = __builtin_bit_cast(
             vec8, *reinterpret_cast<const u32x4*>(kd + k_off[s & 1] + 8704 * kt + 64 * (s >> 1)));
-        sacc[kt] = E::mfma32(ka, qf[s], sacc[kt]);
+        sacc[kt] = E::mfma32(ka, qf[s], s == 0 ? z : sacc[kt]);
       }
     }
+  };
+  // Online softmax of the scores in sacc; the probabilities are packed to the
+  // element type into ppk (one u32x4 per 16-key MFMA step).
+  u32x4 ppk[C::PST];
+  auto softmax = [&]() {
     float mx = sacc[0][0];
 #pragma unroll
     for (int kt = 0; kt < C::NKT; ++kt)
@@ -564,21 +599,25 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     }
     float ls = 0.0f;
 #pragma unroll
-    for (int kt = 0; kt < C::NKT; ++kt)
+    for (int st = 0; st < C::PST; ++st) {
+      const int kt = st >> 1, ip = st & 1;
+      float pv[8];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][r], qk_scale, -mrow));
-        sacc[kt][r] = pv;
-        ls += pv;
+      for (int e = 0; e < 8; ++e) {
+        pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][8 * ip + e], qk_scale, -mrow));
+        ls += pv[e];
       }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ppk[st][e] = cvt_pk<E>(pv[2 * e], pv[2 * e + 1]);
+    }
     lrow += ls;
+  };
+  // O^T += V^T P^T.
+  auto pv_update = [&](const char* vd) {
 #pragma unroll
     for (int st = 0; st < C::PST; ++st) {
       const int kt = st >> 1, ip = st & 1;
-      u32x4 pk;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) pk[e] = cvt_pk<E>(sacc[kt][8 * ip + 2 * e], sacc[kt][8 * ip + 2 * e + 1]);
-      const vec8 pf = __builtin_bit_cast(vec8, pk);
+      const vec8 pf = __builtin_bit_cast(vec8, ppk[st]);
 #pragma unroll
       for (int dt = 0; dt < C::NDT; ++dt) {
         const uint16_t* pv = reinterpret_cast<const uint16_t*>(vd + v_off[dt] + (32 * kt + 16 * ip) * 256);
@@ -592,27 +631,187 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   // Block ids are wave-uniform: read them through the scalar cache.
   typedef __attribute__((address_space(4))) const int32_t const_i32;
   const_i32* irow_s = (const_i32*)irow;
-  auto block_id = [&](int i) { return irow_s[(int64_t)i * a.is[3]]; };
+  auto block_id = [&](int i) { return irow_s[(int64_t)(i < count ? i : count - 1) * a.is[3]]; };
   auto valid = [&](int id_) { return (unsigned)id_ < (unsigned)a.nkb; };
+  auto safe = [&](int id_) { return valid(id_) ? id_ : 0; };
 
-  // Step i: load block i+1 into the other stage, compute block i (skipped,
-  // by a uniform branch, when its id is out of range), barrier.  The other
-  // stage held block i-1, last read before the previous barrier.
-  int cur = block_id(0);
-  load_block(valid(cur) ? cur : 0, ks0, vs0);
-  int nxt = block_id(count > 1 ? 1 : 0);
-  __syncthreads();
-  auto step = [&](char* kc, char* vc, char* kn, char* vn, int i) {
-    const int nn = block_id(i + 2 < count ? i + 2 : count - 1);
-    if (i + 1 < count) load_block(valid(nxt) ? nxt : 0, kn, vn);
-    if (valid(cur)) compute(kc, vc);
+  if constexpr (C::WAVES == 8) {
+    // Ping-pong schedule.  Waves 0-3 (group 0) and 4-7 (group 1) share the
+    // four SIMDs pairwise (wave w and w+4 on one SIMD), and group 1 runs one
+    // phase behind group 0.  Phases alternate between an MFMA phase
+    // M(i) = {O += V(i)^T P(i); S(i+1) = K(i+1) Q^T} and a VALU phase
+    // X(i) = softmax(i) -> P(i), so in every slot one wave of a SIMD issues
+    // MFMAs while the other runs its softmax:
+    //   slot 0      : g0 S(0) X(0)      | g1 S(0)
+    //   slot 2i+1   : g0 M(i)           | g1 X(i)
+    //   slot 2i+2   : g0 X(i+1)         | g1 M(i)
+    // Every wave runs the same sequence S(0) X(0) | M(0) | X(1) | M(1) | ...
+    // with a barrier between phases; group 1 takes one extra barrier before
+    // X(0) and group 0 one after its last phase, which sets the offset.
+    //
+    // LDS stage j (= i % 2) holds {V(i), K(i+1)}; K(0) sits in ks1 until
+    // slot 1.  Group 0 alone loads the stages: during its M(i) (slot 2i+1,
+    // after every read of the stage being replaced completed in slot 2i) it
+    // issues one 1 KiB DMA per two MFMAs for {V(i+1), K(i+2)}, and waits for
+    // them at the end of its X(i+1), so a load has the rest of its slot plus
+    // one more to land.  No other barrier waits for memory.
+    //
+    // An M phase is one basic block: its 32 MFMAs take their LDS operands
+    // four MFMAs ahead, pinned by sched_group_barrier.  A block id that is
+    // out of range is fetched as block 0 and gets all-zero probabilities, so
+    // it adds nothing (for finite block-0 data) and needs no branch.
+    const int grp = wave_s >> 2;
+    const int gw = wave_s & 3;          // wave within group 0
+    constexpr int LPW = 2 * C::CPW;     // chunks of one block per group-0 wave
+    constexpr int NPV = C::PST * C::NDT;
+    constexpr int NU = NPV + C::DS * C::NKT;
+    constexpr int LA = 4;
+    static_assert(4 * LPW <= NU, "an M phase issues one load per two MFMAs");
+    auto barrier = [&]() {
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto wait_loads = [&]() {
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vm0();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    auto lds_addr = [&](char* p) { return (uint32_t)(uintptr_t)(lds_void*)p; };
+    const uint32_t a_ks0 = lds_addr(ks0), a_ks1 = lds_addr(ks1), a_vs0 = lds_addr(vs0), a_vs1 = lds_addr(vs1);
+    // Chunk n of a group-0 wave's share of a stage: n < LPW is V, else K.
+    auto dma = [&](int n, const char* vb, const char* kb, uint32_t vn, uint32_t kn) {
+      if (n < LPW) {
+        const int c = gw * LPW + n;
+        dma16(vb + 8 * c * D, v_src, vn + c * 1024);
+      } else {
+        const int c = gw * LPW + n - LPW;
+        dma16(kb + 8 * c * D, k_src, kn + c * 1088);
+      }
+    };
+    auto block_ptr = [&](const uint16_t* head, int blk) {
+      return reinterpret_cast<const char*>(head + (int64_t)blk * BS * D);
+    };
+    // A operand of MFMA u of an M phase: the V^T tile of P V step
+    // (st, dt) = (u / NDT, u % NDT) for u < NPV, else the K tile of S step
+    // (s, kt) = ((u - NPV) / NKT, (u - NPV) % NKT).
+    auto read_op = [&](int u, const char* vc, const char* kc) {
+      if (u < NPV) {
+        const int st = u / C::NDT, dt = u % C::NDT, kt = st >> 1, ip = st & 1;
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(vc + v_off[dt] + (32 * kt + 16 * ip) * 256);
+        const u32x2 lo = lds_read_tr(p), hi = lds_read_tr(p + 4 * 128);
+        return __builtin_bit_cast(vec8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+      }
+      const int w = u - NPV, s = w / C::NKT, kt = w % C::NKT;
+      return __builtin_bit_cast(vec8,
+                                *reinterpret_cast<const u32x4*>(kc + k_off[s & 1] + 8704 * kt + 64 * (s >> 1)));
+    };
+    f32x16 zero16;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) zero16[r] = 0.0f;
+    auto mfma_u = [&](int u, const vec8& op) {
+      if (u < NPV) {
+        const int st = u / C::NDT, dt = u % C::NDT;
+        o[dt] = E::mfma32(op, __builtin_bit_cast(vec8, ppk[st]), o[dt]);
+      } else {
+        const int w = u - NPV, s = w / C::NKT, kt = w % C::NKT;
+        sacc[kt] = E::mfma32(op, qf[s], s == 0 ? zero16 : sacc[kt]);
+      }
+    };
+    auto m_phase = [&](auto loads, const char* vc, const char* kc, uint32_t vn, uint32_t kn, int bv, int bk) {
+      constexpr bool LOADS = decltype(loads)::value != 0;
+      const char* vb = block_ptr(vhead, bv);
+      const char* kb = block_ptr(khead, bk);
+      vec8 opb[LA];
+#pragma unroll
+      for (int u = 0; u < LA; ++u) opb[u] = read_op(u, vc, kc);
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const vec8 op = opb[u % LA];
+        if (u + LA < NU) opb[u % LA] = read_op(u + LA, vc, kc);
+        mfma_u(u, op);
+        if constexpr (LOADS) {
+          if (u & 1) dma(u >> 1, vb, kb, vn, kn);
+        }
+      }
+      sched_m_phase<NPV, NU, LA, LOADS>();
+    };
+    auto x_phase = [&](int blk) {
+      if (valid(blk)) {
+        softmax();
+      } else {
+#pragma unroll
+        for (int st = 0; st < C::PST; ++st) ppk[st] = u32x4{0u, 0u, 0u, 0u};
+      }
+    };
+    int id_c = block_id(0), id_n = block_id(1), id_nn = block_id(2);
+    if (grp == 0) {
+      const char* vb0 = block_ptr(vhead, safe(id_c));
+      const char* kb0 = block_ptr(khead, safe(id_c));
+      const char* kb1 = block_ptr(khead, safe(id_n));
+#pragma unroll
+      for (int n = 0; n < LPW; ++n) {
+        dma(n, vb0, kb0, a_vs0, a_ks1);
+        dma(n + LPW, vb0, kb0, a_vs0, a_ks1);
+        dma(n + LPW, vb0, kb1, a_vs0, a_ks0);
+      }
+      wait_vm0();
+    }
     __syncthreads();
-    cur = nxt;
-    nxt = nn;
-  };
-  for (int i = 0; i < count; i += 2) {
-    step(ks0, vs0, ks1, vs1, i);
-    if (i + 1 < count) step(ks1, vs1, ks0, vs0, i + 1);
+    scores(ks1);
+    if (grp == 1) barrier();
+    x_phase(id_c);
+    auto pair = [&](int i, const char* vc, const char* kc, uint32_t vn, uint32_t kn) {
+      barrier();
+      if (grp == 0)
+        m_phase(Stage<1>(), vc, kc, vn, kn, safe(id_n), safe(id_nn));
+      else
+        m_phase(Stage<0>(), vc, kc, vn, kn, 0, 0);
+      barrier();
+      if (i + 1 < count) x_phase(id_n);
+      if (grp == 0) wait_loads();
+      id_c = id_n;
+      id_n = id_nn;
+      id_nn = block_id(i + 3);
+    };
+    for (int i = 0; i < count; i += 2) {
+      pair(i, vs0, ks0, a_vs1, a_ks1);
+      if (i + 1 < count) pair(i + 1, vs1, ks1, a_vs0, a_ks0);
+    }
+    if (grp == 0) barrier();
+  } else {
+    // One wave per SIMD: plain double buffering, block i+1 loaded while
+    // block i is computed.
+    auto load_block = [&](int blk, char* kd, char* vd) {
+      const char* kb = reinterpret_cast<const char*>(khead + (int64_t)blk * BS * D);
+      const char* vb = reinterpret_cast<const char*>(vhead + (int64_t)blk * BS * D);
+#pragma unroll
+      for (int j = 0; j < C::CPW; ++j) {
+        const int c = wave_s * C::CPW + j;
+        __builtin_amdgcn_global_load_lds(kb + 8 * c * D + k_src, (lds_void*)(kd + c * 1088), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vb + 8 * c * D + v_src, (lds_void*)(vd + c * 1024), 16, 0, 0);
+      }
+    };
+    int cur = block_id(0);
+    load_block(safe(cur), ks0, vs0);
+    int nxt = block_id(1);
+    __syncthreads();
+    auto step = [&](char* kc, char* vc, char* kn, char* vn, int i) {
+      const int nn = block_id(i + 2);
+      if (i + 1 < count) load_block(safe(nxt), kn, vn);
+      if (valid(cur)) {
+        scores(kc);
+        softmax();
+        pv_update(vc);
+      }
+      __syncthreads();
+      cur = nxt;
+      nxt = nn;
+    };
+    for (int i = 0; i < count; i += 2) {
+      step(ks0, vs0, ks1, vs1, i);
+      if (i + 1 < count) step(ks1, vs1, ks0, vs0, i + 1);
+    }
   }
 
   // Merge the two key halves (waves kh = 0 and kh = 1 of the same qq).
