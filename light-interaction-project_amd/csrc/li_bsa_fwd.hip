@@ -93,6 +93,10 @@ __device__ __forceinline__ int kperm(int i) { return (i & 0x13) | ((i & 4) << 1)
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
+// Lambdas of the kernels are always inlined: an outlined one would pass the
+// accumulators through scratch memory.
+#define LI_INLINE __attribute__((always_inline))
+
 // Transposing LDS load (ds_read_b64_tr_b16) of 4 x 16-bit elements.
 __device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
   typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -449,7 +453,6 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_addr) : "memory");
 }
 __device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
 // Scheduling pins of an M phase (one basic block): the operand reads of the
 // first LA MFMAs, then per MFMA u: the MFMA, the reads of MFMA u + LA (two
 // transposing reads for a P V step, one 16-byte read for an S step) and, when
@@ -562,7 +565,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
 
   // Score tile S^T = K Q^T of one block (this wave's key half).
   f32x16 sacc[C::NKT];
-  auto scores = [&](const char* kd) {
+  auto scores = [&](const char* kd) LI_INLINE {
     f32x16 z;
 #pragma unroll
     for (int r = 0; r < 16; ++r) z[r] = 0.0f;
@@ -578,16 +581,42 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   };
   // Online softmax of the scores in sacc; the probabilities are packed to the
   // element type into ppk (one u32x4 per 16-key MFMA step).
+  //
+  // The exponentials are taken against the running max mrow as it stands.
+  // Only when a lane's partial row sum exceeds 2^20 (some score above mrow + 20
+  // in log2 units; this includes the first block, where mrow = -inf, and
+  // non-finite scores) does the wave take the slow path: block max across
+  // both half-waves, raise mrow, rescale O and l, redo the exponentials.  So
+  // probabilities stay below 2^20 (O, l and the bf16 P far from overflow) and
+  // the block max is not computed at all on the common path; the result is
+  // the same softmax.
   u32x4 ppk[C::PST];
-  auto softmax = [&]() {
-    float mx = sacc[0][0];
+  auto exps = [&]() LI_INLINE {
+    float ls = 0.0f;
 #pragma unroll
-    for (int kt = 0; kt < C::NKT; ++kt)
+    for (int st = 0; st < C::PST; ++st) {
+      const int kt = st >> 1, ip = st & 1;
+      float pv[8];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, sacc[kt][r]);
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-    mx = __builtin_fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * qk_scale;
-    if (__ballot(mx > mrow + 8.0f)) {
+      for (int e = 0; e < 8; ++e) pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][8 * ip + e], qk_scale, -mrow));
+      float s2 = (pv[0] + pv[1]) + (pv[2] + pv[3]);
+      float s3 = (pv[4] + pv[5]) + (pv[6] + pv[7]);
+      ls += s2 + s3;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ppk[st][e] = cvt_pk<E>(pv[2 * e], pv[2 * e + 1]);
+    }
+    return ls;
+  };
+  auto softmax = [&]() LI_INLINE {
+    float ls = exps();
+    if (__ballot(!(ls <= 1048576.0f))) {
+      float mx = sacc[0][0];
+#pragma unroll
+      for (int kt = 0; kt < C::NKT; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, sacc[kt][r]);
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = __builtin_fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * qk_scale;
       const float mnew = __builtin_fmaxf(mrow, mx);
       const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
       mrow = mnew;
@@ -596,24 +625,12 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-    }
-    float ls = 0.0f;
-#pragma unroll
-    for (int st = 0; st < C::PST; ++st) {
-      const int kt = st >> 1, ip = st & 1;
-      float pv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][8 * ip + e], qk_scale, -mrow));
-        ls += pv[e];
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ppk[st][e] = cvt_pk<E>(pv[2 * e], pv[2 * e + 1]);
+      ls = exps();
     }
     lrow += ls;
   };
   // O^T += V^T P^T.
-  auto pv_update = [&](const char* vd) {
+  auto pv_update = [&](const char* vd) LI_INLINE {
 #pragma unroll
     for (int st = 0; st < C::PST; ++st) {
       const int kt = st >> 1, ip = st & 1;
@@ -631,9 +648,9 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   // Block ids are wave-uniform: read them through the scalar cache.
   typedef __attribute__((address_space(4))) const int32_t const_i32;
   const_i32* irow_s = (const_i32*)irow;
-  auto block_id = [&](int i) { return irow_s[(int64_t)(i < count ? i : count - 1) * a.is[3]]; };
-  auto valid = [&](int id_) { return (unsigned)id_ < (unsigned)a.nkb; };
-  auto safe = [&](int id_) { return valid(id_) ? id_ : 0; };
+  auto block_id = [&](int i) LI_INLINE { return irow_s[(int64_t)(i < count ? i : count - 1) * a.is[3]]; };
+  auto valid = [&](int id_) LI_INLINE { return (unsigned)id_ < (unsigned)a.nkb; };
+  auto safe = [&](int id_) LI_INLINE { return valid(id_) ? id_ : 0; };
 
   if constexpr (C::WAVES == 8) {
     // Ping-pong schedule.  Waves 0-3 (group 0) and 4-7 (group 1) share the
@@ -667,20 +684,20 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     constexpr int NU = NPV + C::DS * C::NKT;
     constexpr int LA = 4;
     static_assert(4 * LPW <= NU, "an M phase issues one load per two MFMAs");
-    auto barrier = [&]() {
+    auto barrier = [&]() LI_INLINE {
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
     };
-    auto wait_loads = [&]() {
+    auto wait_loads = [&]() LI_INLINE {
       __builtin_amdgcn_sched_barrier(0);
       wait_vm0();
       __builtin_amdgcn_sched_barrier(0);
     };
-    auto lds_addr = [&](char* p) { return (uint32_t)(uintptr_t)(lds_void*)p; };
+    auto lds_addr = [&](char* p) LI_INLINE { return (uint32_t)(uintptr_t)(lds_void*)p; };
     const uint32_t a_ks0 = lds_addr(ks0), a_ks1 = lds_addr(ks1), a_vs0 = lds_addr(vs0), a_vs1 = lds_addr(vs1);
     // Chunk n of a group-0 wave's share of a stage: n < LPW is V, else K.
-    auto dma = [&](int n, const char* vb, const char* kb, uint32_t vn, uint32_t kn) {
+    auto dma = [&](int n, const char* vb, const char* kb, uint32_t vn, uint32_t kn) LI_INLINE {
       if (n < LPW) {
         const int c = gw * LPW + n;
         dma16(vb + 8 * c * D, v_src, vn + c * 1024);
@@ -689,13 +706,13 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
         dma16(kb + 8 * c * D, k_src, kn + c * 1088);
       }
     };
-    auto block_ptr = [&](const uint16_t* head, int blk) {
+    auto block_ptr = [&](const uint16_t* head, int blk) LI_INLINE {
       return reinterpret_cast<const char*>(head + (int64_t)blk * BS * D);
     };
     // A operand of MFMA u of an M phase: the V^T tile of P V step
     // (st, dt) = (u / NDT, u % NDT) for u < NPV, else the K tile of S step
     // (s, kt) = ((u - NPV) / NKT, (u - NPV) % NKT).
-    auto read_op = [&](int u, const char* vc, const char* kc) {
+    auto read_op = [&](int u, const char* vc, const char* kc) LI_INLINE {
       if (u < NPV) {
         const int st = u / C::NDT, dt = u % C::NDT, kt = st >> 1, ip = st & 1;
         const uint16_t* p = reinterpret_cast<const uint16_t*>(vc + v_off[dt] + (32 * kt + 16 * ip) * 256);
@@ -709,7 +726,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     f32x16 zero16;
 #pragma unroll
     for (int r = 0; r < 16; ++r) zero16[r] = 0.0f;
-    auto mfma_u = [&](int u, const vec8& op) {
+    auto mfma_u = [&](int u, const vec8& op) LI_INLINE {
       if (u < NPV) {
         const int st = u / C::NDT, dt = u % C::NDT;
         o[dt] = E::mfma32(op, __builtin_bit_cast(vec8, ppk[st]), o[dt]);
@@ -718,8 +735,11 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
         sacc[kt] = E::mfma32(op, qf[s], s == 0 ? zero16 : sacc[kt]);
       }
     };
-    auto m_phase = [&](auto loads, const char* vc, const char* kc, uint32_t vn, uint32_t kn, int bv, int bk) {
-      constexpr bool LOADS = decltype(loads)::value != 0;
+    // Both groups run the same M-phase code; the stage DMAs are masked to
+    // group 0 by a per-lane predicate (exec mask), so the accumulators keep
+    // one register assignment across the two groups.
+    const bool loader = tid < 4 * 64;
+    auto m_phase = [&](const char* vc, const char* kc, uint32_t vn, uint32_t kn, int bv, int bk) LI_INLINE {
       const char* vb = block_ptr(vhead, bv);
       const char* kb = block_ptr(khead, bk);
       vec8 opb[LA];
@@ -730,13 +750,13 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
         const vec8 op = opb[u % LA];
         if (u + LA < NU) opb[u % LA] = read_op(u + LA, vc, kc);
         mfma_u(u, op);
-        if constexpr (LOADS) {
-          if (u & 1) dma(u >> 1, vb, kb, vn, kn);
+        if (u & 1) {
+          if (loader) dma(u >> 1, vb, kb, vn, kn);
         }
       }
-      sched_m_phase<NPV, NU, LA, LOADS>();
+      sched_m_phase<NPV, NU, LA, false>();
     };
-    auto x_phase = [&](int blk) {
+    auto x_phase = [&](int blk) LI_INLINE {
       if (valid(blk)) {
         softmax();
       } else {
@@ -761,12 +781,9 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     scores(ks1);
     if (grp == 1) barrier();
     x_phase(id_c);
-    auto pair = [&](int i, const char* vc, const char* kc, uint32_t vn, uint32_t kn) {
+    auto pair = [&](int i, const char* vc, const char* kc, uint32_t vn, uint32_t kn) LI_INLINE {
       barrier();
-      if (grp == 0)
-        m_phase(Stage<1>(), vc, kc, vn, kn, safe(id_n), safe(id_nn));
-      else
-        m_phase(Stage<0>(), vc, kc, vn, kn, 0, 0);
+      m_phase(vc, kc, vn, kn, safe(id_n), safe(id_nn));
       barrier();
       if (i + 1 < count) x_phase(id_n);
       if (grp == 0) wait_loads();
@@ -782,7 +799,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   } else {
     // One wave per SIMD: plain double buffering, block i+1 loaded while
     // block i is computed.
-    auto load_block = [&](int blk, char* kd, char* vd) {
+    auto load_block = [&](int blk, char* kd, char* vd) LI_INLINE {
       const char* kb = reinterpret_cast<const char*>(khead + (int64_t)blk * BS * D);
       const char* vb = reinterpret_cast<const char*>(vhead + (int64_t)blk * BS * D);
 #pragma unroll
@@ -796,7 +813,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     load_block(safe(cur), ks0, vs0);
     int nxt = block_id(1);
     __syncthreads();
-    auto step = [&](char* kc, char* vc, char* kn, char* vn, int i) {
+    auto step = [&](char* kc, char* vc, char* kn, char* vn, int i) LI_INLINE {
       const int nn = block_id(i + 2);
       if (i + 1 < count) load_block(safe(nxt), kn, vn);
       if (valid(cur)) {
