@@ -36,6 +36,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=16, help="heads timed for the CPU baseline sample")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--compare-dense", action="store_true",
+                    help="also time this kernel with every block kept (same kernel symbol as the sparse "
+                         "launches, so it is off by default to keep per-kernel profiles clean)")
     ap.add_argument("--profile", action="store_true",
                     help="launch each kernel of the call --steps times (and a 256 MiB copy for counter "
                          "calibration) for rocprofv3, then print per-launch algorithmic bytes/FLOPs")
@@ -43,19 +46,48 @@ def parse():
 
 
 def event_loop(fn, iters, stream):
-    """Average ms of ``fn`` over ``iters`` launches, timed with events on ``stream``; also per-call ms list."""
+    """Times ``iters`` back-to-back calls of ``fn``.
+
+    Returns (wall ms per call over the whole loop, bracketed by device
+    synchronisation on both sides; per-call GPU ms from events recorded on
+    ``stream``, the stream the library launches on).
+    """
     import torch
 
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
     for i in range(iters):
         starts[i].record(stream)
         fn()
         ends[i].record(stream)
     torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / iters
     per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return sum(per) / len(per), per
+    return wall, per
+
+
+def mean(xs):
+    return sum(xs) / len(xs)
+
+
+def load_traffic(kernel):
+    """HBM bytes per launch of ``kernel`` from the committed counter summary, or None.
+
+    The summary (profiles/bsa_fwd_hy_traffic.md) holds rocprofv3 FETCH_SIZE and
+    WRITE_SIZE per dispatch, each scaled by the factor the same counter reads
+    for a copy kernel of known size in the same run.
+    """
+    path = os.path.join(REPO, "profiles", "bsa_fwd_hy_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch") and kernel in line:
+                    return float(line.split("=")[1].split()[0])
+    except OSError:
+        return None
+    return None
 
 
 def pct(xs, p):
@@ -91,13 +123,6 @@ def main():
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    out = None
-    for _ in range(args.steps):
-        out = step()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     step_ms, per_step = event_loop(step, args.steps, stream)
 
     # Work actually retained: counts from the emitted block lists.
@@ -118,7 +143,8 @@ def main():
     attn = lambda: _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs)  # noqa: E731
     for _ in range(5):
         attn()
-    attn_ms, attn_per = event_loop(attn, args.steps, stream)
+    _, attn_per = event_loop(attn, args.steps, stream)
+    attn_ms = mean(attn_per)   # average launch duration (events on the launch stream)
     attn_tflops = flops / (attn_ms * 1e-3) / 1e12
 
     if args.profile:
@@ -129,14 +155,24 @@ def main():
     sdpa = lambda: torch.nn.functional.scaled_dot_product_attention(qd, kd, vd)  # noqa: E731
     for _ in range(3):
         sdpa()
-    dense_ms, _ = event_loop(sdpa, max(5, args.steps // 5), stream)
+    _, dense_per = event_loop(sdpa, max(5, args.steps // 5), stream)
+    dense_ms = mean(dense_per)
     dense_flops = 4.0 * wl.lq * wl.lk * D * H * B
-    all_ind = torch.arange(g.nk_blk, dtype=torch.int32, device=dev).expand(B, H, g.nq_blk, g.nk_blk).contiguous()
-    all_cnt = torch.full((B, H, g.nq_blk), g.nk_blk, dtype=torch.int32, device=dev)
-    full = lambda: _core.bsa_forward(qf, kf, vf, all_ind, all_cnt, scale, bs)  # noqa: E731
-    full()
-    full_ms, _ = event_loop(full, max(5, args.steps // 5), stream)
-    full_flops = float(B * H * g.nq_blk * g.nk_blk) * 4.0 * bs * bs * D
+    dense = {"torch_sdpa_ms": round(dense_ms, 4),
+             "torch_sdpa_tflops": round(dense_flops / (dense_ms * 1e-3) / 1e12, 2),
+             "speedup_call_vs_sdpa": round(dense_ms / step_ms, 3),
+             "speedup_attention_vs_sdpa": round(dense_ms / attn_ms, 3)}
+    if args.compare_dense:
+        all_ind = torch.arange(g.nk_blk, dtype=torch.int32, device=dev).expand(B, H, g.nq_blk, g.nk_blk).contiguous()
+        all_cnt = torch.full((B, H, g.nq_blk), g.nk_blk, dtype=torch.int32, device=dev)
+        full = lambda: _core.bsa_forward(qf, kf, vf, all_ind, all_cnt, scale, bs)  # noqa: E731
+        full()
+        _, full_per = event_loop(full, max(5, args.steps // 5), stream)
+        full_ms = mean(full_per)
+        full_flops = float(B * H * g.nq_blk * g.nk_blk) * 4.0 * bs * bs * D
+        dense["own_kernel_all_blocks_ms"] = round(full_ms, 4)
+        dense["own_kernel_all_blocks_tflops"] = round(full_flops / (full_ms * 1e-3) / 1e12, 2)
+    kname = "bsa_fwd_dma_kernel<bf16,128>" if (D == 128 and bs in (64, 128)) else f"bsa_fwd_kernel<bf16,{bs},{D}>"
 
     gather_bytes = 2.0 * (wl.lq + 2 * wl.lk) * H * D * B + 2.0 * (g.nq_blk + 2 * g.nk_blk) * bs * H * D * B
 
@@ -157,21 +193,19 @@ def main():
                    "tile": list(wl.tile), "keep_ratio": wl.ratio, "block_size": bs, "nq_blocks": g.nq_blk,
                    "nk_blocks": g.nk_blk, "kept_blocks_per_row_mean": round(float(counts.mean()), 2),
                    "parallelism": "single GPU"},
-        "ms_per_call": {"median": round(pct(per_step, 50), 4), "p10": round(pct(per_step, 10), 4),
-                        "p90": round(pct(per_step, 90), 4), "host_wall": round(wall_ms, 4)},
+        "ms_per_call_gpu": {"mean": round(mean(per_step), 4), "median": round(pct(per_step, 50), 4),
+                            "p10": round(pct(per_step, 10), 4), "p90": round(pct(per_step, 90), 4),
+                            "note": "events around each call on the launch stream; ms_per_step is wall clock"},
         "attention_kernel": {"ms": round(attn_ms, 4), "median_ms": round(pct(attn_per, 50), 4),
                              "tflops": round(attn_tflops, 2),
                              "pct_bf16_peak": round(100.0 * attn_tflops / PEAK_BF16_TFLOPS, 2),
                              "retained_gflop": round(flops / 1e9, 2)},
-        "dense_comparator": {"torch_sdpa_ms": round(dense_ms, 4),
-                             "torch_sdpa_tflops": round(dense_flops / (dense_ms * 1e-3) / 1e12, 2),
-                             "own_kernel_all_blocks_ms": round(full_ms, 4),
-                             "own_kernel_all_blocks_tflops": round(full_flops / (full_ms * 1e-3) / 1e12, 2),
-                             "speedup_call_vs_sdpa": round(dense_ms / step_ms, 3),
-                             "speedup_attention_vs_sdpa": round(dense_ms / attn_ms, 3)},
-        "roofline": {"bound": "mfma", "kernel": "bsa_fwd_kernel<bf16,128,128>",
+        "dense_comparator": dense,
+        "roofline": {"bound": "mfma", "kernel": kname,
                      "achieved": round(attn_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": load_traffic(kname) if args.workload == "hy" else None,
+                     "traffic_unit": "bytes per launch (HBM/MALL side, rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
         "gather_bytes_per_call": gather_bytes,
     }
 

@@ -147,7 +147,10 @@ int li_block_mask(int dtype, int32_t B, int32_t NH, int32_t D,
  * Query tile m (block_size rows) attends to key blocks
  * block_indices[b,h,m,:block_counts[b,h,m]] (each block_size rows of K/V).
  * Zero rows inside kept blocks take part in the softmax, as in the reference.
- * Out-of-range ids are skipped on the device (callers validate beforehand).
+ * Out-of-range ids add nothing and access nothing out of bounds (callers
+ * validate beforehand): the D=64 kernel skips them; the D=128 kernel fetches
+ * block 0 in their place and gives it zero probability (the same result when
+ * block 0 holds finite values).
  * Built for block_size in {64, 128} and D in {64, 128}.
  */
 int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int32_t D,
