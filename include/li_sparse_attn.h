@@ -152,13 +152,28 @@ int li_block_mask(int dtype, int32_t B, int32_t NH, int32_t D,
  * block 0 in their place and gives it zero probability (the same result when
  * block 0 holds finite values).
  * Built for block_size in {64, 128} and D in {64, 128}.
+ *
+ * workspace (optional, device, 16-byte aligned, NULL allowed): scratch of
+ * li_bsa_fwd_workspace_size() bytes.  With it, when the query tiles fill the
+ * device's CUs unevenly, the tiles of the last partial round are each split
+ * into two halves of their block list that run on different CUs and are
+ * combined by a second kernel on the same stream.  Without it (or when it is
+ * smaller than required) every tile runs whole.  Results are the same up to
+ * fp32 rounding of the combination.
  */
 int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int32_t D,
                const void* q, const void* k, const void* v,
                const int32_t* block_indices, const int64_t idx_strides[4], int32_t n_cols,
                const int32_t* block_counts, const int64_t cnt_strides[3],
                float sm_scale, int32_t block_size,
-               void* out, float* lse, void* stream);
+               void* out, float* lse, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes li_bsa_fwd can use for these sizes on the current device
+ * (0: no split applies).  Depends on the device's CU count.  No counterpart
+ * in the reference (its Triton launch has no split).
+ */
+int64_t li_bsa_fwd_workspace_size(int32_t B, int32_t NH, int32_t Lq, int32_t D, int32_t block_size);
 
 #ifdef __cplusplus
 }

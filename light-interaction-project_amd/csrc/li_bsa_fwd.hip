@@ -46,6 +46,8 @@
 //  * Workgroup ids are remapped so that each XCD (ids are dealt round-robin
 //    over the 8 XCDs) processes a contiguous range of (head, tile) work and
 //    the tiles of one head share that XCD's L2 for their K/V blocks.
+#include <mutex>
+
 #include "li_common.hpp"
 
 namespace li {
@@ -63,6 +65,12 @@ struct BsaArgs {
   float* lse;
   int32_t NH, Lq, nkb, nqt, n_cols;
   float qk_scale;
+  // Tail split (D = 128, BS = 128 kernel only): work units u < n_full are
+  // whole query tiles; unit n_full + 2p + half is half `half` of tile
+  // n_full + p (the first or second half of its kept-block list), which
+  // writes unnormalised fp32 O and (m, l) rows to `part` for the merge kernel.
+  int32_t n_full;
+  float* part;
 };
 
 template <int BS, int D>
@@ -496,11 +504,22 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   const int qq = wave >> 1, kh = wave & 1;
   const int l32 = lane & 31, hl = lane >> 5;
 
-  const int nwg = gridDim.x, id = blockIdx.x;
-  const int xcd = id & 7, slot = id >> 3;
-  const int per = nwg >> 3, rem = nwg & 7;
-  const int w = xcd * per + (xcd < rem ? xcd : rem) + slot;
-  const int bh = w / a.nqt, m = w % a.nqt;
+  // Work unit -> query tile.  Ids below n_full are whole tiles, remapped so
+  // that each XCD (ids are dealt round-robin over the 8 XCDs) takes a
+  // contiguous range of them.  The split half-units come last in dispatch
+  // order and keep their natural order, so they spread evenly over the XCDs;
+  // unit n_full + 2p + half is half `half` of tile n_full + p.
+  const int id = blockIdx.x;
+  int tile, half = -1;
+  if (id < a.n_full) {
+    const int xcd = id & 7, slot = id >> 3;
+    const int per = a.n_full >> 3, rem = a.n_full & 7;
+    tile = xcd * per + (xcd < rem ? xcd : rem) + slot;
+  } else {
+    tile = a.n_full + ((id - a.n_full) >> 1);
+    half = (id - a.n_full) & 1;
+  }
+  const int bh = tile / a.nqt, m = tile % a.nqt;
   const int b = bh / a.NH, h = bh % a.NH;
 
   const uint16_t* qhead = a.q + (int64_t)bh * a.Lq * D;
@@ -511,9 +530,26 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   int count = a.cnt[b * a.cs[0] + h * a.cs[1] + (int64_t)m * a.cs[2]];
   count = count < 0 ? 0 : (count > a.n_cols ? a.n_cols : count);
   count = __builtin_amdgcn_readfirstlane(count);
+  if (half >= 0) {
+    const int h0 = (count + 1) >> 1;
+    irow += half ? (int64_t)h0 * a.is[3] : 0;
+    count = half ? count - h0 : h0;
+  }
   const int row0 = m * BS;
+  // Partial rows of a split unit: O as [128 rows][128 d] fp32, then (m, l).
+  float* part_o = half >= 0 ? a.part + (int64_t)(2 * (tile - a.n_full) + half) * BS * (D + 2) : nullptr;
+  float* part_ml = half >= 0 ? part_o + BS * D : nullptr;
 
   if (count == 0) {
+    if (half >= 0) {
+      for (int u = tid; u < BS * D / 4; u += C::NTHR)
+        reinterpret_cast<f32x4*>(part_o)[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int r = tid; r < BS; r += C::NTHR) {
+        part_ml[2 * r] = -__builtin_inff();
+        part_ml[2 * r + 1] = 0.0f;
+      }
+      return;
+    }
     for (int u = tid; u < BS * (D / 8); u += C::NTHR) {
       const int r = row0 + u / (D / 8);
       if (r < a.Lq) *reinterpret_cast<u32x4*>(ohead + (int64_t)r * D + 8 * (u % (D / 8))) = u32x4{0u, 0u, 0u, 0u};
@@ -848,11 +884,33 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   if (kh == 0) {
     const float m1 = xm[lane], l1 = xm[64 + lane];
     const float mm = __builtin_fmaxf(mrow, m1);
-    const float a0 = __builtin_amdgcn_exp2f(mrow - mm), a1 = __builtin_amdgcn_exp2f(m1 - mm);
+    // A row whose blocks were all out of range has mm = -inf: it gets zeros.
+    const bool none = mm == -__builtin_inff();
+    const float a0 = none ? 0.0f : __builtin_amdgcn_exp2f(mrow - mm);
+    const float a1 = none ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
     const float l = lrow * a0 + l1 * a1;
-    const float inv = 1.0f / l;
-    const int r = row0 + 32 * qq + l32;
-    if (r < a.Lq) {
+    const int rt = 32 * qq + l32;
+    if (half >= 0) {
+      float* prow = part_o + rt * D;
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+          f32x4 val;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int rr = 4 * i4 + j;
+            val[j] = o[dt][rr] * a0 + xo[(dt * 16 + rr) * 64 + lane] * a1;
+          }
+          *reinterpret_cast<f32x4*>(prow + 32 * dt + 8 * i4 + 4 * hl) = val;
+        }
+      if (hl == 0) {
+        part_ml[2 * rt] = mm;
+        part_ml[2 * rt + 1] = l;
+      }
+    } else if (row0 + rt < a.Lq) {
+      const int r = row0 + rt;
+      const float inv = l > 0.0f ? 1.0f / l : 0.0f;
       uint16_t* orow = ohead + (int64_t)r * D;
 #pragma unroll
       for (int dt = 0; dt < C::NDT; ++dt)
@@ -867,15 +925,57 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
           const u32x2 pk = {cvt_pk<E>(val[0], val[1]), cvt_pk<E>(val[2], val[3])};
           *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i4 + 4 * hl) = pk;
         }
-      if (a.lse && hl == 0) a.lse[(int64_t)bh * a.Lq + r] = mm + __builtin_log2f(l);
+      if (a.lse && hl == 0) a.lse[(int64_t)bh * a.Lq + r] = none ? -__builtin_inff() : mm + __builtin_log2f(l);
     }
   }
 }
 
+// Combines the two halves of each split query tile: O = (O0 a0 + O1 a1) /
+// (l0 a0 + l1 a1) with a_i = 2^(m_i - max(m0, m1)); lse = max + log2(l).  One
+// workgroup per split tile, two threads per row (64 d each).
+template <typename E>
+__global__ __launch_bounds__(256) void bsa_merge_kernel(BsaArgs a) {
+  constexpr int BS = 128, D = 128;
+  const int p = blockIdx.x;
+  const int tile = a.n_full + p;
+  const int bh = tile / a.nqt, m = tile % a.nqt;
+  const int rt = threadIdx.x >> 1, dh = threadIdx.x & 1;
+  const int r = m * BS + rt;
+  if (r >= a.Lq) return;
+  const float* p0 = a.part + (int64_t)(2 * p) * BS * (D + 2);
+  const float* p1 = p0 + BS * (D + 2);
+  const float m0 = p0[BS * D + 2 * rt], l0 = p0[BS * D + 2 * rt + 1];
+  const float m1 = p1[BS * D + 2 * rt], l1 = p1[BS * D + 2 * rt + 1];
+  const float mm = __builtin_fmaxf(m0, m1);
+  const bool none = mm == -__builtin_inff();
+  const float a0 = none ? 0.0f : __builtin_amdgcn_exp2f(m0 - mm);
+  const float a1 = none ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
+  const float l = l0 * a0 + l1 * a1;
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  const f32x4* o0 = reinterpret_cast<const f32x4*>(p0 + rt * D + 64 * dh);
+  const f32x4* o1 = reinterpret_cast<const f32x4*>(p1 + rt * D + 64 * dh);
+  uint16_t* orow = a.out + ((int64_t)bh * a.Lq + r) * D + 64 * dh;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const f32x4 x0 = o0[2 * i], x1 = o1[2 * i], y0 = o0[2 * i + 1], y1 = o1[2 * i + 1];
+    u32x4 pk;
+    pk[0] = cvt_pk<E>((x0[0] * a0 + x1[0] * a1) * inv, (x0[1] * a0 + x1[1] * a1) * inv);
+    pk[1] = cvt_pk<E>((x0[2] * a0 + x1[2] * a1) * inv, (x0[3] * a0 + x1[3] * a1) * inv);
+    pk[2] = cvt_pk<E>((y0[0] * a0 + y1[0] * a1) * inv, (y0[1] * a0 + y1[1] * a1) * inv);
+    pk[3] = cvt_pk<E>((y0[2] * a0 + y1[2] * a1) * inv, (y0[3] * a0 + y1[3] * a1) * inv);
+    *reinterpret_cast<u32x4*>(orow + 8 * i) = pk;
+  }
+  if (a.lse && dh == 0) a.lse[(int64_t)bh * a.Lq + r] = none ? -__builtin_inff() : mm + __builtin_log2f(l);
+}
+
 template <typename E, int BS>
 int launch_bsa_dma(BsaArgs& a, int tiles, hipStream_t s) {
+  const int nsplit = tiles - a.n_full;
   clear_launch_error();
-  hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, BS>), dim3(tiles), dim3(DmaCfg<BS>::NTHR), 0, s, a);
+  hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, BS>), dim3(a.n_full + 2 * nsplit), dim3(DmaCfg<BS>::NTHR), 0, s, a);
+  if constexpr (BS == 128) {
+    if (nsplit > 0) hipLaunchKernelGGL(bsa_merge_kernel<E>, dim3(nsplit), dim3(256), 0, s, a);
+  }
   return launch_status();
 }
 
@@ -895,15 +995,49 @@ int dispatch_bsa(BsaArgs& a, int bs, int D, int tiles, hipStream_t s) {
   return LI_ERR_UNSUPPORTED;
 }
 
+// Compute units of the current device, cached per device.
+int device_cus() {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+    cached[dev] = n > 0 ? n : -1;
+  }
+  return cached[dev] > 0 ? cached[dev] : 0;
+}
+
+// Query tiles whose block lists are split in two.  With one 8-wave
+// workgroup per CU, `tiles` whole tiles take ceil(tiles / cus) rounds; when
+// the last round holds r <= cus/2 tiles, splitting those r tiles into 2r half
+// units makes that round half as long.
+int64_t split_tiles(int64_t tiles, int cus) {
+  if (cus <= 0 || tiles <= cus) return 0;
+  const int64_t r = tiles % cus;
+  return (r > 0 && 2 * r <= cus) ? r : 0;
+}
+
+constexpr int64_t kPartBytesPerTile = 2 * 128 * (128 + 2) * 4;
+
 }  // namespace
 }  // namespace li
 
 using namespace li;
 
+extern "C" int64_t li_bsa_fwd_workspace_size(int32_t B, int32_t NH, int32_t Lq, int32_t D, int32_t block_size) {
+  if (B <= 0 || NH <= 0 || Lq <= 0 || D != 128 || block_size != 128) return 0;
+  const int64_t tiles = (int64_t)((Lq + block_size - 1) / block_size) * B * NH;
+  return split_tiles(tiles, device_cus()) * kPartBytesPerTile;
+}
+
 extern "C" int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int32_t D, const void* q,
                           const void* k, const void* v, const int32_t* block_indices, const int64_t idx_strides[4],
                           int32_t n_cols, const int32_t* block_counts, const int64_t cnt_strides[3], float sm_scale,
-                          int32_t block_size, void* out, float* lse, void* stream) {
+                          int32_t block_size, void* out, float* lse, void* workspace, int64_t workspace_bytes,
+                          void* stream) {
   if (!q || !k || !v || !block_indices || !idx_strides || !block_counts || !cnt_strides || !out)
     return LI_ERR_INVALID_ARG;
   if (B <= 0 || NH <= 0 || Lq < 0 || Lk < 0 || D <= 0 || n_cols < 0 || block_size <= 0) return LI_ERR_INVALID_ARG;
@@ -933,6 +1067,15 @@ extern "C" int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t 
   a.nqt = (int32_t)nqt;
   a.n_cols = n_cols;
   a.qk_scale = sm_scale * 1.44269504f;
+  a.n_full = (int32_t)tiles;
+  a.part = nullptr;
+  if (workspace && D == 128 && block_size == 128 && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0) {
+    const int64_t ns = split_tiles(tiles, device_cus());
+    if (ns > 0 && workspace_bytes >= ns * kPartBytesPerTile) {
+      a.n_full = (int32_t)(tiles - ns);
+      a.part = static_cast<float*>(workspace);
+    }
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == LI_DTYPE_BF16) return dispatch_bsa<Bf16>(a, block_size, D, (int)tiles, s);
   return dispatch_bsa<F16>(a, block_size, D, (int)tiles, s);

@@ -199,8 +199,11 @@ def block_mask(q_pool, k_pool, *, metric, budget_mode, ratio, nh, nw, num_txt_bl
     return indices, counts
 
 
-def bsa_forward(q, k, v, indices, counts, sm_scale, block_size, return_lse=False, out=None):
-    """Block-sparse attention over contiguous (B,H,L,D) tensors (see li_bsa_fwd); no host sync."""
+def bsa_forward(q, k, v, indices, counts, sm_scale, block_size, return_lse=False, out=None, split=True):
+    """Block-sparse attention over contiguous (B,H,L,D) tensors (see li_bsa_fwd); no host sync.
+
+    ``split=False`` runs every query tile whole (no tail split workspace).
+    """
     dev = _device_check(q, k, v, indices, counts)
     _same_dtype(q, k, v)
     if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
@@ -219,10 +222,16 @@ def bsa_forward(q, k, v, indices, counts, sm_scale, block_size, return_lse=False
     if out is None:
         out = torch.empty_like(q)
     lse = torch.empty((B, NH, Lq), dtype=torch.float32, device=dev) if return_lse else None
+    # Scratch for splitting the query tiles of a partial last round (through
+    # torch's caching allocator; stream-ordered, so it may be freed on return).
+    with torch.cuda.device(dev):
+        ws_bytes = int(lib.li_bsa_fwd_workspace_size(B, NH, Lq, D, int(block_size))) if split else 0
+    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev) if ws_bytes > 0 else None
     st = lib.li_bsa_fwd(dtype_code(q), B, NH, Lq, Lk, D, q.data_ptr(), k.data_ptr(), v.data_ptr(),
                         indices.data_ptr(), i64_array(indices.stride()), indices.shape[3], counts.data_ptr(),
                         i64_array(counts.stride()), float(sm_scale), int(block_size), out.data_ptr(),
-                        lse.data_ptr() if lse is not None else None, _stream(dev))
+                        lse.data_ptr() if lse is not None else None,
+                        ws.data_ptr() if ws is not None else None, ws_bytes, _stream(dev))
     if st == _lib.LI_ERR_K_LEN:
         raise ValueError(f"K Length ({Lk}) must be divisible by logical_block_size ({block_size})")
     check("li_bsa_fwd", st)

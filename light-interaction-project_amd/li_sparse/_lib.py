@@ -16,7 +16,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL below)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libli_sparse_attn.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 LI_OK = 0
 LI_ERR_INVALID_ARG = -1
@@ -70,7 +70,8 @@ SIGNATURES = {
     "li_block_mask": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p,
                                      ctypes.POINTER(MaskParams), _vp, _vp, _vp, _vp]),
     "li_bsa_fwd": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64p, _i32,
-                                  _vp, _i64p, ctypes.c_float, _i32, _vp, _vp, _vp]),
+                                  _vp, _i64p, ctypes.c_float, _i32, _vp, _vp, _vp, _i64, _vp]),
+    "li_bsa_fwd_workspace_size": (ctypes.c_int64, [_i32, _i32, _i32, _i32, _i32]),
 }
 
 

@@ -89,6 +89,50 @@ def test_full_hy_shape_sampled_tiles(dev):
     assert err <= TOL
 
 
+def test_tail_split_matches_whole_tiles_and_oracle(dev):
+    """Tiles of a partial last round run as two halves of their block list plus a merge kernel."""
+    from li_sparse import _lib
+
+    bs, D, B, H, nq, nkb = 128, 128, 1, 3, 100, 12
+    Lq, Lk = nq * bs - 40, nkb * bs
+    print(f"[gpu] bsa tail split B={B} H={H} Lq={Lq} Lk={Lk}", flush=True)
+    tiles = B * H * nq
+    with torch.cuda.device(dev):
+        ws = _lib.lib.li_bsa_fwd_workspace_size(B, H, Lq, D, bs)
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    r = tiles % cus if tiles > cus else 0
+    nsplit = r if 0 < r <= cus // 2 else 0
+    assert ws == nsplit * 2 * 128 * 130 * 4
+    rng = np.random.default_rng(5)
+    q, k, v = _inputs(41, B, H, Lq, Lk, D)
+    ind, cnt = _random_lists(rng, B, H, nq, nkb, 7)
+    # empty, single-block and two-block lists among the split tiles (the last `nsplit` tiles)
+    flat = cnt.reshape(-1)
+    for j, n in enumerate([0, 1, 2, 0, 1]):
+        if nsplit > j:
+            flat[tiles - 1 - 3 * j] = n
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    ii, cc = torch.from_numpy(ind).to(dev), torch.from_numpy(cnt).to(dev)
+    scale = 1.0 / math.sqrt(D)
+    out_s, lse_s = _core.bsa_forward(qd, kd, vd, ii, cc, scale, bs, return_lse=True, split=True)
+    out_w, lse_w = _core.bsa_forward(qd, kd, vd, ii, cc, scale, bs, return_lse=True, split=False)
+    torch.cuda.synchronize()
+    d_out = (out_s.float() - out_w.float()).abs().max().item()
+    fin = torch.isfinite(lse_w)
+    assert torch.equal(torch.isneginf(lse_s), torch.isneginf(lse_w))
+    d_lse = (lse_s[fin] - lse_w[fin]).abs().max().item()
+    print(f"[gpu]   split vs whole: out {d_out:.3e} lse {d_lse:.3e} ({nsplit} split tiles)", flush=True)
+    assert d_out <= 1e-2 and d_lse <= 1e-4
+    o_ref, lse_ref = oatt.bsa_forward(_f64(q), _f64(k), _f64(v), ind, cnt, scale, bs)
+    err = np.abs(out_s.float().cpu().numpy() - o_ref).max()
+    lse_g = lse_s.cpu().numpy()
+    fin = np.isfinite(lse_ref)
+    assert np.array_equal(np.isneginf(lse_g), ~fin)
+    print(f"[gpu]   vs oracle: max abs err {err:.3e}", flush=True)
+    assert err <= TOL
+    assert np.abs(lse_g[fin] - lse_ref[fin]).max() < 1e-3
+
+
 def test_all_blocks_equals_dense_sdpa(dev):
     print("[gpu] bsa all blocks kept vs torch SDPA (fp32)", flush=True)
     bs, D, H, nq, nkb = 128, 128, 4, 6, 12
