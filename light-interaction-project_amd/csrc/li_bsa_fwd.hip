@@ -46,32 +46,15 @@
 //  * Workgroup ids are remapped so that each XCD (ids are dealt round-robin
 //    over the 8 XCDs) processes a contiguous range of (head, tile) work and
 //    the tiles of one head share that XCD's L2 for their K/V blocks.
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
+#include <type_traits>
 
-#include "li_common.hpp"
+#include "li_bsa_common.hpp"
 
 namespace li {
 namespace {
-
-struct BsaArgs {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
-  const int32_t* idx;
-  int64_t is[4];
-  const int32_t* cnt;
-  int64_t cs[3];
-  uint16_t* out;
-  float* lse;
-  int32_t NH, Lq, nkb, nqt, n_cols;
-  float qk_scale;
-  // Tail split (D = 128, BS = 128 kernel only): work units u < n_full are
-  // whole query tiles; unit n_full + 2p + half is half `half` of tile
-  // n_full + p (the first or second half of its kept-block list), which
-  // writes unnormalised fp32 O and (m, l) rows to `part` for the merge kernel.
-  int32_t n_full;
-  float* part;
-};
 
 template <int BS, int D>
 struct Cfg {
@@ -94,41 +77,6 @@ struct Cfg {
   static constexpr int X_FLOATS = NQW * NDT * 16 * 64;       // epilogue O exchange
   static constexpr int X_BYTES = X_FLOATS * 4 + NQW * 2 * 64 * 4;
   static constexpr int LDS_BYTES = KV_BYTES > X_BYTES ? KV_BYTES : X_BYTES;
-};
-
-// MFMA row i of the score tile reads K row perm(i): bits 2 and 3 swapped.
-__device__ __forceinline__ int kperm(int i) { return (i & 0x13) | ((i & 4) << 1) | ((i & 8) >> 1); }
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
-// Lambdas of the kernels are always inlined: an outlined one would pass the
-// accumulators through scratch memory.
-#define LI_INLINE __attribute__((always_inline))
-
-// Transposing LDS load (ds_read_b64_tr_b16) of 4 x 16-bit elements.
-__device__ __forceinline__ u32x2 lds_read_tr(const uint16_t* p) {
-  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p)));
-}
-
-template <typename E>
-__device__ __forceinline__ uint32_t cvt_pk(float a, float b);
-template <>
-__device__ __forceinline__ uint32_t cvt_pk<Bf16>(float a, float b) {
-  typedef float f2 __attribute__((ext_vector_type(2)));
-  typedef __bf16 h2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), h2));
-}
-template <>
-__device__ __forceinline__ uint32_t cvt_pk<F16>(float a, float b) {
-  typedef float f2 __attribute__((ext_vector_type(2)));
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), h2));
-}
-
-template <int N>
-struct Stage {
-  static constexpr int value = N;
 };
 
 template <typename E, int BS, int D>
@@ -447,20 +395,6 @@ struct DmaCfg {
   static constexpr int NQW = WAVES / 2;
 };
 
-// 16 bytes per lane from global memory (wave-uniform base in SGPRs plus a
-// per-lane byte offset) straight into LDS at lds_addr + 16 * lane
-// (global_load_lds_dwordx4).  Issued as inline assembly so that the
-// compiler's wait-count bookkeeping does not see it: the compiler would
-// otherwise treat every pending LDS DMA as making the LDS counter unordered
-// and drain all operand reads in flight (lgkmcnt(0)) after each one.  Being
-// invisible only makes the compiler's own waits stricter (the extra loads
-// are counted by the hardware), never weaker; the caller publishes the data
-// with wait_vm0() before a barrier.  The s_nop covers the M0-write to LDS-DMA
-// hazard.
-__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds_addr) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_addr) : "memory");
-}
-__device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // Scheduling pins of an M phase (one basic block): the operand reads of the
 // first LA MFMAs, then per MFMA u: the MFMA, the reads of MFMA u + LA (two
 // transposing reads for a P V step, one 16-byte read for an S step) and, when
@@ -986,9 +920,27 @@ int launch_bsa(BsaArgs& a, int tiles, hipStream_t s) {
   return launch_status();
 }
 
+// Kernel for D = 128, BS = 128: the 8-wave ping-pong kernel, or the 4-wave
+// kernel (li_bsa_fwd_w4.hip) when the environment variable LI_BSA_WAVES is 4
+// (read on every call).  The 8-wave kernel is the faster one on MI355X at the
+// shapes measured so far.
+bool use_w4() {
+  const char* e = std::getenv("LI_BSA_WAVES");
+  return e && std::strcmp(e, "4") == 0;
+}
+
+template <typename E>
+int launch_w4(BsaArgs& a, int tiles, hipStream_t s) {
+  const int nsplit = tiles - a.n_full;
+  clear_launch_error();
+  launch_bsa_w4(std::is_same<E, Bf16>::value ? LI_DTYPE_BF16 : LI_DTYPE_F16, a, a.n_full + 2 * nsplit, s);
+  if (nsplit > 0) hipLaunchKernelGGL(bsa_merge_kernel<E>, dim3(nsplit), dim3(256), 0, s, a);
+  return launch_status();
+}
+
 template <typename E>
 int dispatch_bsa(BsaArgs& a, int bs, int D, int tiles, hipStream_t s) {
-  if (bs == 128 && D == 128) return launch_bsa_dma<E, 128>(a, tiles, s);
+  if (bs == 128 && D == 128) return use_w4() ? launch_w4<E>(a, tiles, s) : launch_bsa_dma<E, 128>(a, tiles, s);
   if (bs == 128 && D == 64) return launch_bsa<E, 128, 64>(a, tiles, s);
   if (bs == 64 && D == 128) return launch_bsa_dma<E, 64>(a, tiles, s);
   if (bs == 64 && D == 64) return launch_bsa<E, 64, 64>(a, tiles, s);
