@@ -1,10 +1,13 @@
 """Benchmark: AR-aware 3D block-sparse attention forward on one MI355X.
 
 A step is one ``run_sparse_attention`` call of the HY-WorldPlay decode entry
-point on resident bf16 inputs: Q/K/V tile gather + pool, block mask, block-sparse
-attention, untile.  Default workload (``--workload hy``): B=1, 16 heads, D=128,
-30x52 latent, Lq = 4 frames (6240 tokens), Lk = 12 frames (18720 tokens),
-2x8x8 tiles, 30% keep ratio plus the forced diagonal and sink blocks.
+point on resident bf16 inputs: Q and K block pools, block mask, then one
+block-sparse attention kernel that gathers Q/K/V tiles from token order and
+writes the output in token order (shapes the fused kernel does not take run the
+tiled sequence: tile gather + pool, mask, attention, untile).  Default workload
+(``--workload hy``): B=1, 16 heads, D=128, 30x52 latent, Lq = 4 frames (6240
+tokens), Lk = 12 frames (18720 tokens), 2x8x8 tiles, 30% keep ratio plus the
+forced diagonal and sink blocks.
 
 Prints one JSON line.  ``value`` is TFLOP/s over the retained blocks for the
 whole call; the attention kernel's own rate, its share of the bf16 MFMA peak,
@@ -140,16 +143,30 @@ def main():
     flops = float(counts.sum()) * 4.0 * bs * bs * D
     qf, kf, vf = q_t.flatten(2, 3), k_all.flatten(2, 3), v_all.flatten(2, 3)
     scale = 1.0 / math.sqrt(D)
-    attn = lambda: _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs)  # noqa: E731
+    fused = _pipeline.uses_fused(qd, kd, vd, wl.tile, wl.latent_hw)
+    o_tok = torch.empty_like(qd)
+    tiled_attn = lambda: _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs)  # noqa: E731
+    fused_attn = lambda: _core.bsa_forward_gather(  # noqa: E731
+        qd, kd, vd, None, None, 0, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw, ind, cnt, scale, o_tok)
+    # The roofline kernel is the attention kernel the call launches.
+    attn = fused_attn if fused else tiled_attn
+
+    if args.profile:
+        profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params, ind, cnt, flops, dev)
+        return
+
     for _ in range(5):
         attn()
     _, attn_per = event_loop(attn, args.steps, stream)
     attn_ms = mean(attn_per)   # average launch duration (events on the launch stream)
     attn_tflops = flops / (attn_ms * 1e-3) / 1e12
-
-    if args.profile:
-        profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params, ind, cnt, flops, dev)
-        return
+    tiled_info = None
+    if fused:
+        tiled_attn()
+        _, tiled_per = event_loop(tiled_attn, max(5, args.steps // 5), stream)
+        tiled_ms = mean(tiled_per)
+        tiled_info = {"ms": round(tiled_ms, 4), "tflops": round(flops / (tiled_ms * 1e-3) / 1e12, 2),
+                      "note": "the same attention on pre-gathered tiles (the unfused sequence's kernel)"}
 
     # Dense comparators: torch SDPA (valid tokens) and this kernel with every block kept.
     sdpa = lambda: torch.nn.functional.scaled_dot_product_attention(qd, kd, vd)  # noqa: E731
@@ -172,9 +189,19 @@ def main():
         full_flops = float(B * H * g.nq_blk * g.nk_blk) * 4.0 * bs * bs * D
         dense["own_kernel_all_blocks_ms"] = round(full_ms, 4)
         dense["own_kernel_all_blocks_tflops"] = round(full_flops / (full_ms * 1e-3) / 1e12, 2)
-    kname = "bsa_fwd_dma_kernel<bf16,128>" if (D == 128 and bs in (64, 128)) else f"bsa_fwd_kernel<bf16,{bs},{D}>"
+    if fused:
+        kname = "bsa_fwd_dma_kernel<bf16,128,gather>"
+    elif D == 128 and bs in (64, 128):
+        kname = "bsa_fwd_dma_kernel<bf16,128>"
+    else:
+        kname = f"bsa_fwd_kernel<bf16,{bs},{D}>"
 
-    gather_bytes = 2.0 * (wl.lq + 2 * wl.lk) * H * D * B + 2.0 * (g.nq_blk + 2 * g.nk_blk) * bs * H * D * B
+    # Bytes the call moves outside attention: the pools read Q and K once
+    # (fused); the tiled sequence also writes and re-reads the tiles and untiles.
+    if fused:
+        prep_bytes = 2.0 * (wl.lq + wl.lk) * H * D * B
+    else:
+        prep_bytes = 2.0 * (wl.lq + 2 * wl.lk) * H * D * B + 2.0 * (g.nq_blk + 2 * g.nk_blk) * bs * H * D * B
 
     result = {
         "metric": "sparse-attn fwd ms/call + TFLOPS (% MFMA peak) at HY shape, 30% keep",
@@ -196,17 +223,19 @@ def main():
         "ms_per_call_gpu": {"mean": round(mean(per_step), 4), "median": round(pct(per_step, 50), 4),
                             "p10": round(pct(per_step, 10), 4), "p90": round(pct(per_step, 90), 4),
                             "note": "events around each call on the launch stream; ms_per_step is wall clock"},
-        "attention_kernel": {"ms": round(attn_ms, 4), "median_ms": round(pct(attn_per, 50), 4),
+        "attention_kernel": {"kernel": kname, "ms": round(attn_ms, 4), "median_ms": round(pct(attn_per, 50), 4),
                              "tflops": round(attn_tflops, 2),
                              "pct_bf16_peak": round(100.0 * attn_tflops / PEAK_BF16_TFLOPS, 2),
                              "retained_gflop": round(flops / 1e9, 2)},
+        "attention_kernel_tiled": tiled_info,
         "dense_comparator": dense,
         "roofline": {"bound": "mfma", "kernel": kname,
                      "achieved": round(attn_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": load_traffic(kname) if args.workload == "hy" else None,
                      "traffic_unit": "bytes per launch (HBM/MALL side, rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
-        "gather_bytes_per_call": gather_bytes,
+        "fused_path": fused,
+        "prep_bytes_per_call": prep_bytes,
     }
 
     if not args.no_cpu_baseline:
@@ -218,17 +247,25 @@ def profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params
     """Each kernel of one call, --steps launches apiece, for rocprofv3 kernel traces and counters."""
     import torch
 
-    from li_sparse import _core
+    from li_sparse import _core, _pipeline
     from li_sparse.hy.ar_sparse_operation import fast_generate_indices
 
     B, H, D, bs = wl.batch, wl.heads, wl.head_dim, g.bs
     qf, kf, vf = q_t.flatten(2, 3), k_all.flatten(2, 3), v_all.flatten(2, 3)
+    scale = 1.0 / math.sqrt(D)
     out = torch.empty_like(qf)
     o_lin = torch.empty_like(qd)
+    o_tok = torch.empty_like(qd)
     src = torch.empty(1 << 27, dtype=torch.bfloat16, device=dev).fill_(1.0)   # 256 MiB
     dst = torch.empty_like(src)
+    fused = _pipeline.uses_fused(qd, kd, vd, wl.tile, wl.latent_hw)
     for _ in range(args.steps):
-        _core.bsa_forward(qf, kf, vf, ind, cnt, 1.0 / math.sqrt(D), bs, out=out)
+        if fused:   # the call's own sequence: pools, mask, fused attention
+            _core.pool(qd, q_p, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+            _core.pool(kd, k_p, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+            _core.bsa_forward_gather(qd, kd, vd, None, None, 0, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh,
+                                     g.nw, ind, cnt, scale, o_tok)
+        _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs, out=out)
         _core.q_prep(qd, q_t, q_p, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
         _core.kv_prep(kd, vd, k_all, v_all, k_p, 0, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
         fast_generate_indices(q_p, k_p, 0, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), params, dev)
@@ -241,7 +278,10 @@ def profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params
         "algorithmic_per_launch": {
             "bsa_fwd_kernel": {"flop": flops,
                                "bytes_min": e * (wl.lq + 2 * wl.lk) * H * D * B,
-                               "note": "FLOPs = sum(counts) * 4 * BS^2 * D; bytes_min = Q + K + V read once"},
+                               "note": "FLOPs = sum(counts) * 4 * BS^2 * D; bytes_min = Q + K + V read once; "
+                                       "the fused (gather) and tiled instantiations do the same work"},
+            "gather_pool_kernel<1> pool only (Q)": {"bytes": e * H * D * B * wl.lq + e * H * D * g.nq_blk},
+            "gather_pool_kernel<1> pool only (K)": {"bytes": e * H * D * B * wl.lk + e * H * D * g.nk_blk},
             "gather_pool_kernel<1> (Q)": {"bytes": e * H * D * B * (wl.lq + g.nq_blk * bs) + e * H * D * g.nq_blk},
             "gather_pool_kernel<2> (K,V)": {"bytes": e * H * D * B * 2 * (wl.lk + g.nk_blk * bs)
                                             + e * H * D * g.nk_blk},

@@ -86,6 +86,18 @@ int li_kv_prep(int dtype, int32_t B, int32_t NH, int32_t D,
                const li_tile_geom* geom, void* stream);
 
 /*
+ * Tile mean pool without writing tiles: the pooling half of launch_q_prep /
+ * launch_kv_prep (HYAR:58-70, 110-122) for the fused attention path, whose
+ * kernel reads tokens in tile order straight from the untiled tensors.
+ *   src (B, NH, L, D) any strides; mean (B, NH, nblk, D), written at block (blk + pool_off);
+ *   same values, bit for bit, as the mean written by li_q_prep / li_kv_prep.
+ */
+int li_pool(int dtype, int32_t B, int32_t NH, int32_t D,
+            const void* src, const int64_t src_strides[4],
+            void* mean, const int64_t mean_strides[4], int64_t pool_off,
+            const li_tile_geom* geom, void* stream);
+
+/*
  * Untile scatter.  Replaces launch_untile(src, dst, T, H, W, tt, th, tw, nh, nw)
  * and _fused_untile_kernel (HYAR:127-161, 204-218; MGS:109-140, 168-177).
  *   src (B, NH, nblk, BS, D) tiles, any strides; dst (B, NH, L, D), any strides.
@@ -167,6 +179,37 @@ int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int32_t
                const int32_t* block_counts, const int64_t cnt_strides[3],
                float sm_scale, int32_t block_size,
                void* out, float* lse, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Block-sparse attention with the tile gather and untile fused into the
+ * kernel: the whole of run_sparse_attention's tile / attend / untile
+ * sequence (HYAR:330-361; the tiles of HYAR:26-161 are never written).
+ *   q (B, NH, Lq, D), k / v (B, NH, Lk, D), out (B, NH, Lq, D): untiled
+ *     tokens, any batch/head/token strides (multiples of 8 elements, unit d
+ *     stride, 16-byte aligned); token t*H*W + h*W + w of the grids in
+ *     q_geom / k_geom (T = frames of each, other fields equal).  Tokens
+ *     outside the grid read as zeros; out is written at valid tokens only.
+ *   k_txt / v_txt: (B, NH, num_txt_blk*BS, D) contiguous zero-padded text
+ *     keys/values (block ids < num_txt_blk), or NULL when num_txt_blk = 0;
+ *     visual block vb has id num_txt_blk + vb.
+ *   block_indices / block_counts as for li_bsa_fwd, over the q_geom tiles.
+ *   lse (B, NH, nq_blk*BS) fp32 per tiled query row, or NULL.
+ *   workspace as for li_bsa_fwd (same size function with Lq = nq_blk*BS).
+ * Same results as li_q_prep + li_kv_prep + li_bsa_fwd + li_untile, bit for
+ * bit.  Built for D = 128, BS = tt*th*tw = 128, tw and W multiples of 4
+ * (LI_ERR_UNSUPPORTED otherwise).  No counterpart in the reference as one
+ * call.
+ */
+int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D,
+                      const void* q, const int64_t q_strides[4],
+                      const void* k, const int64_t k_strides[4],
+                      const void* v, const int64_t v_strides[4],
+                      const void* k_txt, const void* v_txt, int32_t num_txt_blk,
+                      const li_tile_geom* q_geom, const li_tile_geom* k_geom,
+                      const int32_t* block_indices, const int64_t idx_strides[4], int32_t n_cols,
+                      const int32_t* block_counts, const int64_t cnt_strides[3],
+                      float sm_scale, void* out, const int64_t out_strides[4], float* lse,
+                      void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Workspace bytes li_bsa_fwd can use for these sizes on the current device

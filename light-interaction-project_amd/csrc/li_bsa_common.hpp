@@ -5,6 +5,27 @@
 
 namespace li {
 
+// Token-order addressing of the fused path, in which the tiled Q/K/V/O
+// buffers are never materialised: tile row f of block blk of a (t, h, w) grid
+// is token l = t*H*W + h*W + w with (t, h, w) = (ct*tt + ft, ch*th + fh,
+// cw*tw + fw), (ct, ch, cw) = (blk / (nh*nw), (blk / nw) % nh, blk % nw) and
+// (ft, fh, fw) = (f / (th*tw), (f / tw) % th, f % tw) (the tile permutation of
+// hy-worldplay/.../ar_sparse_operation.py:42-59); tokens outside the grid
+// read as zeros and are not stored.  q, out and the visual k, v are
+// (B, NH, L, D) views with element strides (d stride 1); key blocks with ids
+// below ntxt are text blocks, read from zero-padded (B, NH, ntxt*BS, D)
+// buffers; visual block vb has id ntxt + vb.
+struct BsaGather {
+  int64_t qs[3], os[3], ks[3], vs[3];  // batch, head, token strides
+  const uint16_t* ktxt;
+  const uint16_t* vtxt;
+  int32_t ntxt;
+  int32_t H, W, tt, th, tw, nh, nw, Tq, Tk;
+  // ceil(2^32 / d) for d = nh*nw, nw, th*tw, tw (0 for d = 1): x / d ==
+  // umulhi(x, magic) exactly for x, d < 2^16.
+  uint32_t mg_nhnw, mg_nw, mg_thtw, mg_tw;
+};
+
 // Kernel arguments of the attention forward (all pointers are device
 // pointers; strides in elements).
 struct BsaArgs {
@@ -25,6 +46,8 @@ struct BsaArgs {
   // writes unnormalised fp32 O and (m, l) rows to `part` for the merge kernel.
   int32_t n_full;
   float* part;
+  // Fused path only (kernel template flag); unused otherwise.
+  BsaGather g;
 };
 
 // Launches the 4-wave D = 128, BS = 128 kernel for units [0, a.n_full) whole
@@ -81,7 +104,55 @@ struct Stage {
 __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds_addr) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_addr) : "memory");
 }
+// The same load with an instruction offset imm (it must fold to a constant in
+// [0, 4096)), which the hardware adds to both the global address
+// (sbase + voff + imm) and the LDS address (m0 + imm + 16 * lane).
+__device__ __forceinline__ void dma16_imm(const void* sbase, uint32_t voff, uint32_t m0_addr, int imm) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 offset:%3" ::"v"(voff), "s"(sbase), "{m0}"(m0_addr),
+               "i"(imm)
+               : "memory");
+}
+// dma16_imm from one of two sources chosen by bit `bit` of the wave-uniform
+// `mask`: (sa, va) when it is set, else (sb, vb).  Three scalar instructions
+// and one vector select; they also cover the M0-write hazard.
+__device__ __forceinline__ void dma16_sel(uint32_t mask, int bit, const void* sa, uint32_t va, const void* sb,
+                                          uint32_t vb, uint32_t m0_addr, int imm) {
+  const void* base;
+  uint64_t lm;
+  uint32_t voff;
+  asm volatile(
+      "s_bitcmp1_b32 %[mask], %[bit]\n\t"
+      "s_cselect_b64 %[base], %[sa], %[sb]\n\t"
+      "s_cselect_b64 %[lm], -1, 0\n\t"
+      "v_cndmask_b32_e64 %[voff], %[vb], %[va], %[lm]\n\t"
+      "global_load_lds_dwordx4 %[voff], %[base] offset:%[imm]"
+      : [base] "=&s"(base), [lm] "=&s"(lm), [voff] "=&v"(voff)
+      : [mask] "s"(mask), [bit] "i"(bit), [sa] "s"(sa), [sb] "s"(sb), [va] "v"(va), [vb] "v"(vb),
+        "{m0}"(m0_addr), [imm] "i"(imm)
+      : "memory", "scc");
+}
 __device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Token of tile row f of block blk in a grid of T frames; valid = inside.
+// x / d for x, d < 2^16 from magic = ceil(2^32 / d) (0 encodes d = 1).
+// Branch-free: umulhi(x, 0) = 0, and the identity term is x only for magic 0.
+__device__ __forceinline__ uint32_t udiv16(uint32_t x, uint32_t magic) {
+  return __umulhi(x, magic) | (x & (0u - (uint32_t)(magic == 0u)));
+}
+
+__device__ __forceinline__ int32_t tile_token(const BsaGather& g, int32_t T, uint32_t blk, uint32_t f, bool& valid) {
+  const uint32_t ct = udiv16(blk, g.mg_nhnw), rem = blk - ct * (uint32_t)(g.nh * g.nw);
+  const uint32_t ch = udiv16(rem, g.mg_nw), cw = rem - ch * (uint32_t)g.nw;
+  const uint32_t ft = udiv16(f, g.mg_thtw), r = f - ft * (uint32_t)(g.th * g.tw);
+  const uint32_t fh = udiv16(r, g.mg_tw), fw = r - fh * (uint32_t)g.tw;
+  const int32_t t = ct * g.tt + ft, hh = ch * g.th + fh, w = cw * g.tw + fw;
+  valid = t < T && hh < g.H && w < g.W;
+  return (t * g.H + hh) * g.W + w;
+}
+
+// 8 KiB of zeros: the source of DMA chunks that fall outside the grid (chunk
+// j < 8 of a wave reads bytes [1024 j, 1024 j + 1024)).
+__device__ __attribute__((aligned(16))) const uint32_t g_zero_rows[2048] = {0};
 
 }  // namespace
 }  // namespace li

@@ -420,9 +420,10 @@ __device__ __forceinline__ void sched_m_phase() {
   sched_m_units<NPV, NU, LA, LOADS, 0>();
 }
 
-template <typename E, int BS>
+template <typename E, int BS, bool G = false>
 __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   using C = DmaCfg<BS>;
+  static_assert(!G || BS == 128, "token-order addressing is built for 128-row tiles");
   constexpr int D = 128;
   typedef typename E::vec8 vec8;
   typedef __attribute__((address_space(3))) void lds_void;
@@ -474,6 +475,18 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   float* part_o = half >= 0 ? a.part + (int64_t)(2 * (tile - a.n_full) + half) * BS * (D + 2) : nullptr;
   float* part_ml = half >= 0 ? part_o + BS * D : nullptr;
 
+  // Output row of tile row rt, or null when it is not stored (past Lq, or
+  // outside the token grid on the fused path).
+  auto out_row = [&](int rt) LI_INLINE -> uint16_t* {
+    if constexpr (G) {
+      bool ok;
+      const int32_t l = tile_token(a.g, a.g.Tq, m, rt, ok);
+      return ok ? a.out + b * a.g.os[0] + h * a.g.os[1] + (int64_t)l * a.g.os[2] : nullptr;
+    } else {
+      return row0 + rt < a.Lq ? ohead + (int64_t)(row0 + rt) * D : nullptr;
+    }
+  };
+
   if (count == 0) {
     if (half >= 0) {
       for (int u = tid; u < BS * D / 4; u += C::NTHR)
@@ -485,8 +498,8 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       return;
     }
     for (int u = tid; u < BS * (D / 8); u += C::NTHR) {
-      const int r = row0 + u / (D / 8);
-      if (r < a.Lq) *reinterpret_cast<u32x4*>(ohead + (int64_t)r * D + 8 * (u % (D / 8))) = u32x4{0u, 0u, 0u, 0u};
+      uint16_t* orow = out_row(u / (D / 8));
+      if (orow) *reinterpret_cast<u32x4*>(orow + 8 * (u % (D / 8))) = u32x4{0u, 0u, 0u, 0u};
     }
     if (a.lse)
       for (int r = tid; r < BS; r += C::NTHR)
@@ -496,11 +509,19 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
 
   vec8 qf[C::DS];
   {
-    const int r = row0 + 32 * qq + l32;
+    const uint16_t* qrow = nullptr;
+    if constexpr (G) {
+      bool ok;
+      const int32_t l = tile_token(a.g, a.g.Tq, m, 32 * qq + l32, ok);
+      if (ok) qrow = a.q + b * a.g.qs[0] + h * a.g.qs[1] + (int64_t)l * a.g.qs[2];
+    } else {
+      const int r = row0 + 32 * qq + l32;
+      if (r < a.Lq) qrow = qhead + (int64_t)r * D;
+    }
 #pragma unroll
     for (int s = 0; s < C::DS; ++s) {
       u32x4 x = {0u, 0u, 0u, 0u};
-      if (r < a.Lq) x = *reinterpret_cast<const u32x4*>(qhead + (int64_t)r * D + 16 * s + 8 * hl);
+      if (qrow) x = *reinterpret_cast<const u32x4*>(qrow + 16 * s + 8 * hl);
       qf[s] = __builtin_bit_cast(vec8, x);
     }
   }
@@ -511,6 +532,13 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   const int rp = lane >> 4;
   const uint32_t k_src = 2u * (rp * D + 8 * ((lane & 15) ^ rp));
   const uint32_t v_src = 2u * (rp * D + 32 * (((lane & 15) >> 2) ^ rp) + 8 * (lane & 3));
+  // Fused path: the same granules, with the rows of a chunk one token stride
+  // apart in the untiled visual K / V.
+  uint32_t k_src_vis = 0, v_src_vis = 0;
+  if constexpr (G) {
+    k_src_vis = (uint32_t)(rp * a.g.ks[2] * 2) + 16u * ((lane & 15) ^ rp);
+    v_src_vis = (uint32_t)(rp * a.g.vs[2] * 2) + 2u * (32 * (((lane & 15) >> 2) ^ rp) + 8 * (lane & 3));
+  }
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
 
   // K operand byte offsets: row R = KW*kh + kperm(l32) (+32 kt), granule 2s+hl.
@@ -666,18 +694,94 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     };
     auto lds_addr = [&](char* p) LI_INLINE { return (uint32_t)(uintptr_t)(lds_void*)p; };
     const uint32_t a_ks0 = lds_addr(ks0), a_ks1 = lds_addr(ks1), a_vs0 = lds_addr(vs0), a_vs1 = lds_addr(vs1);
-    // Chunk n of a group-0 wave's share of a stage: n < LPW is V, else K.
-    auto dma = [&](int n, const char* vb, const char* kb, uint32_t vn, uint32_t kn) LI_INLINE {
-      if (n < LPW) {
-        const int c = gw * LPW + n;
-        dma16(vb + 8 * c * D, v_src, vn + c * 1024);
-      } else {
-        const int c = gw * LPW + n - LPW;
-        dma16(kb + 8 * c * D, k_src, kn + c * 1088);
-      }
+    // A group-0 wave loads chunks c = gw * LPW + j (j < LPW) of every K and
+    // V block: 1 KiB each, block rows 4c..4c+3.  Each load is one
+    // instruction: scalar base + lane offset + instruction offset
+    // (j & 3) * 1024.
+    //
+    // Tiled blocks, text blocks (contiguous in the padded text buffer) and
+    // out-of-grid chunks (read from g_zero_rows) have contiguous rows: the
+    // base is alt (j < 4) or alt + 4096, the lane offset k_src/v_src.
+    // A visual chunk on the fused path is 4 consecutive tokens along w (tw and
+    // W are multiples of 4), all inside the grid or all outside it.  Its
+    // offset from the block's origin token does not depend on the block, so
+    // each lane keeps the byte offsets of its wave's chunks, less the
+    // instruction offset, in kvo/vvo; a block costs one origin computation and
+    // one ballot for the in-grid mask.  The offsets stay non-negative because
+    // a chunk's token offset is at least 4c when the grid is at least one tile
+    // in each dimension, and a token is at least 256 bytes.
+    static_assert(LPW == 8, "two scalar bases of four chunks each");
+    struct Blk {
+      const char* vis;  // fused path: origin token of a visual block
+      const char* alt;  // contiguous source at this wave's first chunk
+      uint32_t mask;    // bit j: chunk j of this wave is an in-grid visual chunk
     };
-    auto block_ptr = [&](const uint16_t* head, int blk) LI_INLINE {
-      return reinterpret_cast<const char*>(head + (int64_t)blk * BS * D);
+
+    uint32_t kvo[LPW], vvo[LPW];
+    uint32_t lane_ft = 0, lane_fh = 0, lane_fw = 0;
+    const char* vis_k = nullptr;
+    const char* vis_v = nullptr;
+    const char* txt_k = nullptr;
+    const char* txt_v = nullptr;
+    const char* zero_rows = reinterpret_cast<const char*>(g_zero_rows);
+    if constexpr (G) {
+      vis_k = reinterpret_cast<const char*>(a.k + b * a.g.ks[0] + h * a.g.ks[1]);
+      vis_v = reinterpret_cast<const char*>(a.v + b * a.g.vs[0] + h * a.g.vs[1]);
+      txt_k = reinterpret_cast<const char*>(a.g.ktxt + (int64_t)bh * a.g.ntxt * BS * D) + gw * LPW * 1024;
+      txt_v = reinterpret_cast<const char*>(a.g.vtxt + (int64_t)bh * a.g.ntxt * BS * D) + gw * LPW * 1024;
+      const uint32_t thtw = a.g.th * a.g.tw;
+      auto coords = [&](uint32_t c, uint32_t& ft, uint32_t& fh, uint32_t& fw) LI_INLINE {
+        ft = udiv16(4 * c, a.g.mg_thtw);
+        const uint32_t r = 4 * c - ft * thtw;
+        fh = udiv16(r, a.g.mg_tw);
+        fw = r - fh * (uint32_t)a.g.tw;
+      };
+#pragma unroll
+      for (int j = 0; j < LPW; ++j) {
+        uint32_t ft, fh, fw;
+        coords(gw * LPW + j, ft, fh, fw);
+        const uint32_t coff = (ft * a.g.H + fh) * a.g.W + fw;
+        kvo[j] = coff * (uint32_t)(2 * a.g.ks[2]) + k_src_vis - (j & 3) * 1024;
+        vvo[j] = coff * (uint32_t)(2 * a.g.vs[2]) + v_src_vis - (j & 3) * 1024;
+      }
+      coords(lane & 31, lane_ft, lane_fh, lane_fw);
+    }
+    auto src_of = [&](int blk, bool is_v) LI_INLINE {
+      Blk s_{nullptr, nullptr, 0u};
+      if constexpr (!G) {
+        s_.alt = reinterpret_cast<const char*>((is_v ? vhead : khead) + (int64_t)blk * BS * D) + gw * LPW * 1024;
+      } else {
+        // Straight-line scalar code: both sides of each choice are computed.
+        const bool txt = blk < a.g.ntxt;
+        const int32_t vbs = blk - a.g.ntxt;
+        const uint32_t vb = (uint32_t)(vbs > 0 ? vbs : 0);
+        const uint32_t ct = udiv16(vb, a.g.mg_nhnw), rem = vb - ct * (uint32_t)(a.g.nh * a.g.nw);
+        const uint32_t ch = udiv16(rem, a.g.mg_nw), cw = rem - ch * (uint32_t)a.g.nw;
+        const uint32_t t0 = ct * a.g.tt, h0 = ch * a.g.th, w0 = cw * a.g.tw;
+        const int64_t l0 = (int64_t)((t0 * a.g.H + h0) * a.g.W + w0);
+        s_.vis = (is_v ? vis_v : vis_k) + l0 * 2 * (is_v ? a.g.vs[2] : a.g.ks[2]);
+        const bool inside = (lane_ft < a.g.Tk - t0) & (lane_fh < a.g.H - h0) & (lane_fw < a.g.W - w0);
+        const uint32_t in_grid = (uint32_t)__ballot(inside);
+        s_.mask = (in_grid >> (gw * LPW)) & (txt ? 0u : (1u << LPW) - 1u);
+        const char* tb = (is_v ? txt_v : txt_k) + (int64_t)blk * (BS * D * 2);
+        s_.alt = txt ? tb : zero_rows;
+      }
+      return s_;
+    };
+    // Chunk n of a group-0 wave's share of a stage: n < LPW is V, else K.
+    auto dma = [&](int n, const Blk& sv, const Blk& sk, uint32_t vn, uint32_t kn) LI_INLINE {
+      const bool isv = n < LPW;
+      const int j = isv ? n : n - LPW;
+      const int c = gw * LPW + j;
+      const int imm = (j & 3) * 1024;
+      const Blk& s_ = isv ? sv : sk;
+      const uint32_t m0 = (isv ? vn + c * 1024 : kn + c * 1088) - imm;
+      const uint32_t lin = isv ? v_src : k_src;
+      const char* alt = j < 4 ? s_.alt : s_.alt + 4096;
+      if constexpr (!G)
+        dma16_imm(alt, lin, m0, imm);
+      else
+        dma16_sel(s_.mask, j, s_.vis, isv ? vvo[j] : kvo[j], alt, lin, m0, imm);
     };
     // A operand of MFMA u of an M phase: the V^T tile of P V step
     // (st, dt) = (u / NDT, u % NDT) for u < NPV, else the K tile of S step
@@ -705,13 +809,15 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
         sacc[kt] = E::mfma32(op, qf[s], s == 0 ? zero16 : sacc[kt]);
       }
     };
-    // Both groups run the same M-phase code; the stage DMAs are masked to
-    // group 0 by a per-lane predicate (exec mask), so the accumulators keep
-    // one register assignment across the two groups.
-    const bool loader = tid < 4 * 64;
-    auto m_phase = [&](const char* vc, const char* kc, uint32_t vn, uint32_t kn, int bv, int bk) LI_INLINE {
-      const char* vb = block_ptr(vhead, bv);
-      const char* kb = block_ptr(khead, bk);
+    // M phase; group 0 (load = true) also issues the stage DMAs, group 1
+    // runs the same MFMAs and reads without them.  Each is one basic block.
+    auto m_phase = [&](const char* vc, const char* kc, uint32_t vn, uint32_t kn, int bv, int bk,
+                       bool load) LI_INLINE {
+      Blk vb{nullptr, nullptr, 0u}, kb{nullptr, nullptr, 0u};
+      if (load) {
+        vb = src_of(bv, true);
+        kb = src_of(bk, false);
+      }
       vec8 opb[LA];
 #pragma unroll
       for (int u = 0; u < LA; ++u) opb[u] = read_op(u, vc, kc);
@@ -720,9 +826,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
         const vec8 op = opb[u % LA];
         if (u + LA < NU) opb[u % LA] = read_op(u + LA, vc, kc);
         mfma_u(u, op);
-        if (u & 1) {
-          if (loader) dma(u >> 1, vb, kb, vn, kn);
-        }
+        if (load && (u & 1)) dma(u >> 1, vb, kb, vn, kn);
       }
       sched_m_phase<NPV, NU, LA, false>();
     };
@@ -736,9 +840,9 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     };
     int id_c = block_id(0), id_n = block_id(1), id_nn = block_id(2);
     if (grp == 0) {
-      const char* vb0 = block_ptr(vhead, safe(id_c));
-      const char* kb0 = block_ptr(khead, safe(id_c));
-      const char* kb1 = block_ptr(khead, safe(id_n));
+      const Blk vb0 = src_of(safe(id_c), true);
+      const Blk kb0 = src_of(safe(id_c), false);
+      const Blk kb1 = src_of(safe(id_n), false);
 #pragma unroll
       for (int n = 0; n < LPW; ++n) {
         dma(n, vb0, kb0, a_vs0, a_ks1);
@@ -748,24 +852,33 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       wait_vm0();
     }
     __syncthreads();
-    scores(ks1);
-    if (grp == 1) barrier();
-    x_phase(id_c);
-    auto pair = [&](int i, const char* vc, const char* kc, uint32_t vn, uint32_t kn) LI_INLINE {
+    // Each group runs its own copy of the block loop (group 0's with the
+    // stage loads), so neither carries the other's load code and the copies
+    // meet only after the loop.
+    auto pair = [&](int i, const char* vc, const char* kc, uint32_t vn, uint32_t kn, bool load) LI_INLINE {
       barrier();
-      m_phase(vc, kc, vn, kn, safe(id_n), safe(id_nn));
+      m_phase(vc, kc, vn, kn, safe(id_n), safe(id_nn), load);
       barrier();
       if (i + 1 < count) x_phase(id_n);
-      if (grp == 0) wait_loads();
+      if (load) wait_loads();
       id_c = id_n;
       id_n = id_nn;
       id_nn = block_id(i + 3);
     };
-    for (int i = 0; i < count; i += 2) {
-      pair(i, vs0, ks0, a_vs1, a_ks1);
-      if (i + 1 < count) pair(i + 1, vs1, ks1, a_vs0, a_ks0);
-    }
-    if (grp == 0) barrier();
+    auto run = [&](bool load) LI_INLINE {
+      scores(ks1);
+      if (!load) barrier();
+      x_phase(id_c);
+      for (int i = 0; i < count; i += 2) {
+        pair(i, vs0, ks0, a_vs1, a_ks1, load);
+        if (i + 1 < count) pair(i + 1, vs1, ks1, a_vs0, a_ks0, load);
+      }
+      if (load) barrier();
+    };
+    if (grp == 0)
+      run(true);
+    else
+      run(false);
   } else {
     // One wave per SIMD: plain double buffering, block i+1 loaded while
     // block i is computed.
@@ -842,24 +955,27 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
         part_ml[2 * rt] = mm;
         part_ml[2 * rt + 1] = l;
       }
-    } else if (row0 + rt < a.Lq) {
-      const int r = row0 + rt;
-      const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-      uint16_t* orow = ohead + (int64_t)r * D;
+    } else {
+      if (uint16_t* orow = out_row(rt)) {
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
-      for (int dt = 0; dt < C::NDT; ++dt)
+        for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          float val[4];
+          for (int i4 = 0; i4 < 4; ++i4) {
+            float val[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int rr = 4 * i4 + j;
-            val[j] = (o[dt][rr] * a0 + xo[(dt * 16 + rr) * 64 + lane] * a1) * inv;
+            for (int j = 0; j < 4; ++j) {
+              const int rr = 4 * i4 + j;
+              val[j] = (o[dt][rr] * a0 + xo[(dt * 16 + rr) * 64 + lane] * a1) * inv;
+            }
+            const u32x2 pk = {cvt_pk<E>(val[0], val[1]), cvt_pk<E>(val[2], val[3])};
+            *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i4 + 4 * hl) = pk;
           }
-          const u32x2 pk = {cvt_pk<E>(val[0], val[1]), cvt_pk<E>(val[2], val[3])};
-          *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i4 + 4 * hl) = pk;
-        }
-      if (a.lse && hl == 0) a.lse[(int64_t)bh * a.Lq + r] = none ? -__builtin_inff() : mm + __builtin_log2f(l);
+      }
+      // The LSE is in tile-row order and covers the grid's padding rows too
+      // (their queries are zero), whether or not the row has an output token.
+      const int r = row0 + rt;
+      if (a.lse && hl == 0 && r < a.Lq) a.lse[(int64_t)bh * a.Lq + r] = none ? -__builtin_inff() : mm + __builtin_log2f(l);
     }
   }
 }
@@ -867,7 +983,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
 // Combines the two halves of each split query tile: O = (O0 a0 + O1 a1) /
 // (l0 a0 + l1 a1) with a_i = 2^(m_i - max(m0, m1)); lse = max + log2(l).  One
 // workgroup per split tile, two threads per row (64 d each).
-template <typename E>
+template <typename E, bool G = false>
 __global__ __launch_bounds__(256) void bsa_merge_kernel(BsaArgs a) {
   constexpr int BS = 128, D = 128;
   const int p = blockIdx.x;
@@ -876,6 +992,16 @@ __global__ __launch_bounds__(256) void bsa_merge_kernel(BsaArgs a) {
   const int rt = threadIdx.x >> 1, dh = threadIdx.x & 1;
   const int r = m * BS + rt;
   if (r >= a.Lq) return;
+  // Padding rows of the grid have no output token but do have an LSE.
+  uint16_t* orow = nullptr;
+  if constexpr (G) {
+    const int b = bh / a.NH, h = bh % a.NH;
+    bool ok;
+    const int32_t l = tile_token(a.g, a.g.Tq, m, rt, ok);
+    if (ok) orow = a.out + b * a.g.os[0] + h * a.g.os[1] + (int64_t)l * a.g.os[2] + 64 * dh;
+  } else {
+    orow = a.out + ((int64_t)bh * a.Lq + r) * D + 64 * dh;
+  }
   const float* p0 = a.part + (int64_t)(2 * p) * BS * (D + 2);
   const float* p1 = p0 + BS * (D + 2);
   const float m0 = p0[BS * D + 2 * rt], l0 = p0[BS * D + 2 * rt + 1];
@@ -888,9 +1014,8 @@ __global__ __launch_bounds__(256) void bsa_merge_kernel(BsaArgs a) {
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   const f32x4* o0 = reinterpret_cast<const f32x4*>(p0 + rt * D + 64 * dh);
   const f32x4* o1 = reinterpret_cast<const f32x4*>(p1 + rt * D + 64 * dh);
-  uint16_t* orow = a.out + ((int64_t)bh * a.Lq + r) * D + 64 * dh;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < 8 && orow; ++i) {
     const f32x4 x0 = o0[2 * i], x1 = o1[2 * i], y0 = o0[2 * i + 1], y1 = o1[2 * i + 1];
     u32x4 pk;
     pk[0] = cvt_pk<E>((x0[0] * a0 + x1[0] * a1) * inv, (x0[1] * a0 + x1[1] * a1) * inv);
@@ -899,7 +1024,17 @@ __global__ __launch_bounds__(256) void bsa_merge_kernel(BsaArgs a) {
     pk[3] = cvt_pk<E>((y0[2] * a0 + y1[2] * a1) * inv, (y0[3] * a0 + y1[3] * a1) * inv);
     *reinterpret_cast<u32x4*>(orow + 8 * i) = pk;
   }
-  if (a.lse && dh == 0) a.lse[(int64_t)bh * a.Lq + r] = none ? -__builtin_inff() : mm + __builtin_log2f(l);
+  if (a.lse && dh == 0 && r < a.Lq) a.lse[(int64_t)bh * a.Lq + r] = none ? -__builtin_inff() : mm + __builtin_log2f(l);
+}
+
+template <typename E>
+int launch_bsa_gather(BsaArgs& a, int tiles, hipStream_t s) {
+  const int nsplit = tiles - a.n_full;
+  clear_launch_error();
+  hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, 128, true>), dim3(a.n_full + 2 * nsplit), dim3(DmaCfg<128>::NTHR), 0, s,
+                     a);
+  if (nsplit > 0) hipLaunchKernelGGL((bsa_merge_kernel<E, true>), dim3(nsplit), dim3(256), 0, s, a);
+  return launch_status();
 }
 
 template <typename E, int BS>
@@ -1031,4 +1166,115 @@ extern "C" int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t 
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == LI_DTYPE_BF16) return dispatch_bsa<Bf16>(a, block_size, D, (int)tiles, s);
   return dispatch_bsa<F16>(a, block_size, D, (int)tiles, s);
+}
+
+namespace {
+
+uint32_t magic16(int32_t d) { return d == 1 ? 0u : (uint32_t)(((1ull << 32) + (uint64_t)d - 1) / (uint64_t)d); }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// (B, NH, L, D) view usable by the fused kernel: unit d stride, 16-byte rows.
+bool row_view_ok(const void* p, const int64_t st[4]) {
+  return p && aligned16(p) && st[3] == 1 && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 && st[2] > 0;
+}
+
+}  // namespace
+
+extern "C" int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D, const void* q,
+                                 const int64_t q_strides[4], const void* k, const int64_t k_strides[4],
+                                 const void* v, const int64_t v_strides[4], const void* k_txt, const void* v_txt,
+                                 int32_t num_txt_blk, const li_tile_geom* q_geom, const li_tile_geom* k_geom,
+                                 const int32_t* block_indices, const int64_t idx_strides[4], int32_t n_cols,
+                                 const int32_t* block_counts, const int64_t cnt_strides[3], float sm_scale, void* out,
+                                 const int64_t out_strides[4], float* lse, void* workspace, int64_t workspace_bytes,
+                                 void* stream) {
+  if (!q_strides || !k_strides || !v_strides || !out_strides || !q_geom || !k_geom || !block_indices ||
+      !idx_strides || !block_counts || !cnt_strides)
+    return LI_ERR_INVALID_ARG;
+  if (B <= 0 || NH <= 0 || n_cols < 0 || num_txt_blk < 0) return LI_ERR_INVALID_ARG;
+  if (dtype != LI_DTYPE_BF16 && dtype != LI_DTYPE_F16) return LI_ERR_UNSUPPORTED;
+  const li_tile_geom& gq = *q_geom;
+  const li_tile_geom& gk = *k_geom;
+  if (gq.H != gk.H || gq.W != gk.W || gq.tt != gk.tt || gq.th != gk.th || gq.tw != gk.tw || gq.nh != gk.nh ||
+      gq.nw != gk.nw)
+    return LI_ERR_SHAPE;
+  if (gq.H <= 0 || gq.W <= 0 || gq.tt <= 0 || gq.th <= 0 || gq.tw <= 0 || gq.T < 0 || gk.T < 0)
+    return LI_ERR_SHAPE;
+  if (gq.nh != (gq.H + gq.th - 1) / gq.th || gq.nw != (gq.W + gq.tw - 1) / gq.tw) return LI_ERR_SHAPE;
+  // Built for D = 128, 128-token tiles whose w extent and the grid width are
+  // multiples of 4 (a 4-row DMA chunk is 4 consecutive tokens along w).
+  if (D != 128 || gq.tt * gq.th * gq.tw != 128 || gq.tw % 4 != 0 || gq.W % 4 != 0) return LI_ERR_UNSUPPORTED;
+  // The grid is at least one tile high and wide, and K/V tokens do not
+  // overlap, so a chunk's byte offset from its tile's origin is at least
+  // 1024 * (chunk index) (the kernel subtracts the instruction offset).
+  if (gq.H < gq.th || gq.W < gq.tw) return LI_ERR_UNSUPPORTED;
+  if (!row_view_ok(q, q_strides) || !row_view_ok(k, k_strides) || !row_view_ok(v, v_strides) ||
+      !row_view_ok(out, out_strides))
+    return LI_ERR_INVALID_ARG;
+  if (k_strides[2] < D || v_strides[2] < D) return LI_ERR_UNSUPPORTED;
+  if (num_txt_blk > 0 && (!k_txt || !v_txt || !aligned16(k_txt) || !aligned16(v_txt))) return LI_ERR_INVALID_ARG;
+  const int64_t nq = (int64_t)((gq.T + gq.tt - 1) / gq.tt) * gq.nh * gq.nw;
+  const int64_t nkv = (int64_t)((gk.T + gk.tt - 1) / gk.tt) * gk.nh * gk.nw;
+  if ((int64_t)gq.nh * gq.nw >= 65536 || nkv + num_txt_blk >= 65536 || nq >= 65536) return LI_ERR_SHAPE;
+  if ((int64_t)gq.T * gq.H * gq.W >= (1ll << 31) || (int64_t)gk.T * gk.H * gk.W >= (1ll << 31)) return LI_ERR_SHAPE;
+  // The byte offset of a K/V row from its tile's origin token is held in 32
+  // bits: at most max_row tokens, times the token stride, plus one row.
+  const int64_t max_row = (int64_t)(gq.tt - 1) * gq.H * gq.W + (int64_t)(gq.th - 1) * gq.W + gq.tw - 1;
+  const int64_t kv_st = k_strides[2] > v_strides[2] ? k_strides[2] : v_strides[2];
+  if ((max_row * kv_st + D) * 2 > (1ll << 32)) return LI_ERR_SHAPE;
+  if (nq == 0) return LI_OK;
+  const int64_t tiles = nq * B * NH;
+  if (tiles > 0x7FFFFFFF) return LI_ERR_SHAPE;
+  BsaArgs a = {};
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.idx = block_indices;
+  for (int i = 0; i < 4; ++i) a.is[i] = idx_strides[i];
+  a.cnt = block_counts;
+  for (int i = 0; i < 3; ++i) a.cs[i] = cnt_strides[i];
+  a.out = static_cast<uint16_t*>(out);
+  a.lse = lse;
+  a.NH = NH;
+  a.Lq = (int32_t)(nq * 128);
+  a.nkb = (int32_t)(nkv + num_txt_blk);
+  a.nqt = (int32_t)nq;
+  a.n_cols = n_cols;
+  a.qk_scale = sm_scale * 1.44269504f;
+  BsaGather& g = a.g;
+  for (int i = 0; i < 3; ++i) {
+    g.qs[i] = q_strides[i];
+    g.ks[i] = k_strides[i];
+    g.vs[i] = v_strides[i];
+    g.os[i] = out_strides[i];
+  }
+  g.ktxt = static_cast<const uint16_t*>(k_txt);
+  g.vtxt = static_cast<const uint16_t*>(v_txt);
+  g.ntxt = num_txt_blk;
+  g.H = gq.H;
+  g.W = gq.W;
+  g.tt = gq.tt;
+  g.th = gq.th;
+  g.tw = gq.tw;
+  g.nh = gq.nh;
+  g.nw = gq.nw;
+  g.Tq = gq.T;
+  g.Tk = gk.T;
+  g.mg_nhnw = magic16(gq.nh * gq.nw);
+  g.mg_nw = magic16(gq.nw);
+  g.mg_thtw = magic16(gq.th * gq.tw);
+  g.mg_tw = magic16(gq.tw);
+  a.n_full = (int32_t)tiles;
+  a.part = nullptr;
+  if (workspace && aligned16(workspace)) {
+    const int64_t ns = split_tiles(tiles, device_cus());
+    if (ns > 0 && workspace_bytes >= ns * kPartBytesPerTile) {
+      a.n_full = (int32_t)(tiles - ns);
+      a.part = static_cast<float*>(workspace);
+    }
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == LI_DTYPE_BF16) return launch_bsa_gather<Bf16>(a, (int)tiles, s);
+  return launch_bsa_gather<F16>(a, (int)tiles, s);
 }

@@ -76,8 +76,9 @@ __global__ __launch_bounds__(256) void gather_pool_kernel(GatherArgs a) {
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     sbase[n] = a.src[n] + b * a.ss[n][0] + h * a.ss[n][1] + (int64_t)(8 * c) * a.ss[n][3];
-    dbase[n] = a.dst[n] + b * a.ds[n][0] + h * a.ds[n][1] + (blk + a.dst_off) * a.ds[n][2] +
-               (int64_t)(8 * c) * a.ds[n][4];
+    dbase[n] = a.dst[n] ? a.dst[n] + b * a.ds[n][0] + h * a.ds[n][1] + (blk + a.dst_off) * a.ds[n][2] +
+                              (int64_t)(8 * c) * a.ds[n][4]
+                        : nullptr;
   }
 
   float acc[8];
@@ -94,7 +95,7 @@ __global__ __launch_bounds__(256) void gather_pool_kernel(GatherArgs a) {
     for (int n = 0; n < NT; ++n) {
       u32x4 v = {0u, 0u, 0u, 0u};
       if (valid) v = load8(sbase[n] + l * a.ss[n][2], a.ss[n][3], vs);
-      store8(dbase[n] + (int64_t)f * a.ds[n][3], a.ds[n][4], vd, v);
+      if (dbase[n]) store8(dbase[n] + (int64_t)f * a.ds[n][3], a.ds[n][4], vd, v);
       if (n == 0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -257,6 +258,26 @@ extern "C" int li_kv_prep(int dtype, int32_t B, int32_t NH, int32_t D, const voi
   a.vec_src = vec_ok(k_src, k_src_strides, 4) && vec_ok(v_src, v_src_strides, 4);
   a.vec_dst = vec_ok(k_dst, k_dst_strides, 5) && vec_ok(v_dst, v_dst_strides, 5);
   return launch_gather<2>(dtype, B, NH, D, a, geom, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int li_pool(int dtype, int32_t B, int32_t NH, int32_t D, const void* src, const int64_t src_strides[4],
+                       void* mean, const int64_t mean_strides[4], int64_t pool_off, const li_tile_geom* geom,
+                       void* stream) {
+  if (!src || !mean || !src_strides || !mean_strides) return LI_ERR_INVALID_ARG;
+  if (pool_off < 0) return LI_ERR_INVALID_ARG;
+  GatherArgs a = {};
+  a.src[0] = static_cast<const uint16_t*>(src);
+  a.dst[0] = nullptr;
+  for (int i = 0; i < 4; ++i) {
+    a.ss[0][i] = src_strides[i];
+    a.ms[i] = mean_strides[i];
+  }
+  a.mean = static_cast<uint16_t*>(mean);
+  a.dst_off = 0;
+  a.pool_off = pool_off;
+  a.vec_src = vec_ok(src, src_strides, 4);
+  a.vec_dst = 0;
+  return launch_gather<1>(dtype, B, NH, D, a, geom, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int li_untile(int dtype, int32_t B, int32_t NH, int32_t D, const void* src, const int64_t src_strides[5],

@@ -94,6 +94,74 @@ def kv_prep(k_src, v_src, k_dst, v_dst, k_mean, dst_off, pool_off, T, H, W, tt, 
     check("li_kv_prep", st)
 
 
+def pool(src, mean, pool_off, T, H, W, tt, th, tw, nh, nw):
+    """Tile mean pool without writing tiles (see li_pool); same values as q_prep / kv_prep."""
+    dev = _device_check(src, mean)
+    _same_dtype(src, mean)
+    B, NH, L, D = src.shape
+    nblk = num_blocks(T, tt, nh, nw)
+    if L < T * H * W:
+        raise ValueError(f"source length {L} < T*H*W = {T * H * W}")
+    if tuple(mean.shape[:2]) != (B, NH) or mean.shape[2] < nblk + pool_off or mean.shape[3] != D:
+        raise ValueError(f"pool buffer shape {tuple(mean.shape)} does not hold {nblk}+{pool_off} rows of {D}")
+    g = TileGeom(T, H, W, tt, th, tw, nh, nw)
+    st = lib.li_pool(dtype_code(src), B, NH, D, src.data_ptr(), i64_array(src.stride()), mean.data_ptr(),
+                     i64_array(mean.stride()), int(pool_off), ctypes.byref(g), _stream(dev))
+    check("li_pool", st)
+
+
+def fused_supported(D, tile, latent_hw):
+    """Whether li_bsa_fwd_gather covers this shape.
+
+    D = 128, 128-token tiles, tw and W multiples of 4, and a latent grid at
+    least one tile high and wide (H >= th, W >= tw).
+    """
+    tt, th, tw = tile
+    H, W = latent_hw
+    return D == 128 and tt * th * tw == 128 and tw % 4 == 0 and W % 4 == 0 and H >= th and W >= tw
+
+
+def bsa_forward_gather(q, k, v, k_txt, v_txt, num_txt_blk, T_q, T_k, H, W, tt, th, tw, nh, nw, indices, counts,
+                       sm_scale, out, return_lse=False, split=True):
+    """Block-sparse attention reading Q/K/V in token order and writing ``out`` in token order (li_bsa_fwd_gather).
+
+    q/out (B,NH,Lq,D) and k/v (B,NH,Lk,D) views with any strides the kernel accepts; k_txt/v_txt the
+    zero-padded (B,NH,num_txt_blk*BS,D) contiguous text keys/values or None.  No host sync.
+    """
+    dev = _device_check(q, k, v, out, indices, counts)
+    _same_dtype(q, k, v, out)
+    B, NH, Lq, D = q.shape
+    if indices.dtype != torch.int32 or counts.dtype != torch.int32:
+        raise TypeError("block indices and counts must be int32")
+    nq = num_blocks(T_q, tt, nh, nw)
+    if indices.dim() != 4 or tuple(indices.shape[:2]) != (B, NH) or indices.shape[2] < nq:
+        raise ValueError(f"block_indices shape {tuple(indices.shape)} does not cover {nq} query tiles")
+    if counts.dim() != 3 or tuple(counts.shape[:2]) != (B, NH) or counts.shape[2] < nq:
+        raise ValueError(f"block_counts shape {tuple(counts.shape)} does not cover {nq} query tiles")
+    if Lq < T_q * H * W or k.shape[2] < T_k * H * W or tuple(out.shape) != tuple(q.shape):
+        raise ValueError("token tensors do not hold the grids")
+    if num_txt_blk > 0:
+        _same_dtype(q, k_txt, v_txt)
+        if not (k_txt.is_contiguous() and v_txt.is_contiguous()):
+            raise ValueError("padded text K/V must be contiguous")
+    bs = tt * th * tw
+    lse = torch.empty((B, NH, nq * bs), dtype=torch.float32, device=dev) if return_lse else None
+    with torch.cuda.device(dev):
+        ws_bytes = int(lib.li_bsa_fwd_workspace_size(B, NH, nq * bs, D, bs)) if split else 0
+    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev) if ws_bytes > 0 else None
+    gq, gk = TileGeom(T_q, H, W, tt, th, tw, nh, nw), TileGeom(T_k, H, W, tt, th, tw, nh, nw)
+    st = lib.li_bsa_fwd_gather(dtype_code(q), B, NH, D, q.data_ptr(), i64_array(q.stride()), k.data_ptr(),
+                               i64_array(k.stride()), v.data_ptr(), i64_array(v.stride()),
+                               k_txt.data_ptr() if num_txt_blk > 0 else None,
+                               v_txt.data_ptr() if num_txt_blk > 0 else None, int(num_txt_blk), ctypes.byref(gq),
+                               ctypes.byref(gk), indices.data_ptr(), i64_array(indices.stride()), indices.shape[3],
+                               counts.data_ptr(), i64_array(counts.stride()), float(sm_scale), out.data_ptr(),
+                               i64_array(out.stride()), lse.data_ptr() if lse is not None else None,
+                               ws.data_ptr() if ws is not None else None, ws_bytes, _stream(dev))
+    check("li_bsa_fwd_gather", st)
+    return (out, lse) if return_lse else out
+
+
 def untile(src, dst, T, H, W, tt, th, tw, nh, nw):
     """Inverse scatter of tiles into the linear token layout (see li_untile)."""
     dev = _device_check(src, dst)

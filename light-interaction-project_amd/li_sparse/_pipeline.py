@@ -59,12 +59,61 @@ def _stage(events, name):
         events[name] = e
 
 
-def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, events=None):
+def _fusable(*ts):
+    """Token views the fused kernel reads directly: unit d stride, 16-byte aligned, non-overlapping rows."""
+    for t in ts:
+        st = t.stride()
+        if st[3] != 1 or any(x % 8 for x in st[:3]) or st[2] < t.shape[3] or t.data_ptr() % 16:
+            return False
+    return True
+
+
+def uses_fused(q, k_vis, v_vis, tile, latent_hw):
+    """True when ``sparse_attention(..., fused=True)`` takes the fused kernel for these inputs."""
+    return _core.fused_supported(q.shape[3], tile, latent_hw) and _fusable(q, k_vis, v_vis)
+
+
+def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events):
+    """Pools, block selection, then one kernel that gathers, attends and untiles."""
+    B, NH, _, D = q.shape
+    dev, dt = q.device, q.dtype
+    _stage(events, "alloc_start")
+    q_pool = torch.empty((B, NH, g.nq_blk, D), device=dev, dtype=dt)
+    k_pool = torch.empty((B, NH, g.nk_blk, D), device=dev, dtype=dt)
+    kt = vt = None
+    if text_len > 0:
+        pad = g.num_txt_blk * g.bs - text_len
+        kt = (F.pad(k_txt, (0, 0, 0, pad)) if pad > 0 else k_txt).contiguous()
+        vt = (F.pad(v_txt, (0, 0, 0, pad)) if pad > 0 else v_txt).contiguous()
+    o_out = torch.empty_like(q)
+    _stage(events, "alloc_end")
+    _stage(events, "prep_start")
+    _core.pool(q, q_pool, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    _core.pool(k_vis, k_pool, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    _stage(events, "prep_end")
+    _stage(events, "index_start")
+    indices, counts = select(q_pool, k_pool, text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
+    _stage(events, "index_end")
+    _stage(events, "attn_start")
+    _core.bsa_forward_gather(q, k_vis, v_vis, kt, vt, g.num_txt_blk, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw,
+                             g.nh, g.nw, indices, counts, 1.0 / math.sqrt(D), o_out)
+    _stage(events, "attn_end")
+    _stage(events, "untile_start")
+    _stage(events, "untile_end")
+    return o_out if o_out.dtype == out_dtype else o_out.to(out_dtype)
+
+
+def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, events=None, fused=True):
     """One sparse-attention forward.
 
     q (B,H,Lq,D); k_txt/v_txt (B,H,N_txt,D) or None; k_vis/v_vis (B,H,Lk,D), any strides.
     ``select(q_pool, k_pool, text_len, grid_q, grid_k) -> (indices, counts)``.
     ``events`` (dict or None) collects CUDA events per stage for profiling.
+    ``fused`` (default) runs pools + one gather/attend/untile kernel where the
+    shape allows it (D = 128, 128-token tiles, tw and W multiples of 4, a grid
+    at least one tile high and wide, token views with unit d stride);
+    otherwise, or with ``fused=False``, the tiled sequence q_prep / kv_prep /
+    attention / untile.  Both give the same bits.
     """
     out_dtype = q.dtype
     if q.dtype not in (torch.bfloat16, torch.float16):
@@ -75,6 +124,8 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
     g = geometry(latent_hw, tile, q.shape[2], k_vis.shape[2], text_len)
     B, NH, _, D = q.shape
     dev, dt = q.device, q.dtype
+    if fused and uses_fused(q, k_vis, v_vis, tile, (g.H, g.W)):
+        return _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events)
     _stage(events, "alloc_start")
     q_tiled = torch.empty((B, NH, g.nq_blk, g.bs, D), device=dev, dtype=dt)
     q_pool = torch.empty((B, NH, g.nq_blk, D), device=dev, dtype=dt)
