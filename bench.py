@@ -259,35 +259,46 @@ def profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params
     src = torch.empty(1 << 27, dtype=torch.bfloat16, device=dev).fill_(1.0)   # 256 MiB
     dst = torch.empty_like(src)
     fused = _pipeline.uses_fused(qd, kd, vd, wl.tile, wl.latent_hw)
+    q_pool = torch.empty_like(q_p)
+    k_pool = torch.empty_like(k_p)
     for _ in range(args.steps):
-        if fused:   # the call's own sequence: pools, mask, fused attention
-            _core.pool(qd, q_p, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
-            _core.pool(kd, k_p, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+        if fused:
+            # The call's own kernels: Q pool, K pool, block mask, fused
+            # attention (+ its tail merge); then the tiled attention kernel on
+            # the same lists, for comparison.
+            _core.pool(qd, q_pool, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+            _core.pool(kd, k_pool, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+            fast_generate_indices(q_pool, k_pool, 0, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), params, dev)
             _core.bsa_forward_gather(qd, kd, vd, None, None, 0, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh,
                                      g.nw, ind, cnt, scale, o_tok)
-        _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs, out=out)
-        _core.q_prep(qd, q_t, q_p, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
-        _core.kv_prep(kd, vd, k_all, v_all, k_p, 0, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
-        fast_generate_indices(q_p, k_p, 0, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), params, dev)
-        _core.untile(out.view(B, H, g.nq_blk, bs, D), o_lin, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+            _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs, out=out)
+        else:
+            _core.q_prep(qd, q_t, q_p, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+            _core.kv_prep(kd, vd, k_all, v_all, k_p, 0, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+            fast_generate_indices(q_p, k_p, 0, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), params, dev)
+            _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs, out=out)
+            _core.untile(out.view(B, H, g.nq_blk, bs, D), o_lin, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
         dst.copy_(src)
     torch.cuda.synchronize()
     e = 2  # bytes per element
-    print(json.dumps({
-        "profile": wl.name, "launches_per_kernel": args.steps,
-        "algorithmic_per_launch": {
-            "bsa_fwd_kernel": {"flop": flops,
-                               "bytes_min": e * (wl.lq + 2 * wl.lk) * H * D * B,
-                               "note": "FLOPs = sum(counts) * 4 * BS^2 * D; bytes_min = Q + K + V read once; "
-                                       "the fused (gather) and tiled instantiations do the same work"},
-            "gather_pool_kernel<1> pool only (Q)": {"bytes": e * H * D * B * wl.lq + e * H * D * g.nq_blk},
-            "gather_pool_kernel<1> pool only (K)": {"bytes": e * H * D * B * wl.lk + e * H * D * g.nk_blk},
-            "gather_pool_kernel<1> (Q)": {"bytes": e * H * D * B * (wl.lq + g.nq_blk * bs) + e * H * D * g.nq_blk},
-            "gather_pool_kernel<2> (K,V)": {"bytes": e * H * D * B * 2 * (wl.lk + g.nk_blk * bs)
-                                            + e * H * D * g.nk_blk},
-            "untile_kernel": {"bytes": e * H * D * B * 2 * wl.lq},
-            "copy (calibration)": {"bytes_read": src.numel() * e, "bytes_written": dst.numel() * e},
-        }}), flush=True)
+    alg = {
+        "bsa_fwd_kernel": {"flop": flops,
+                           "bytes_min": e * (wl.lq + 2 * wl.lk) * H * D * B,
+                           "note": "FLOPs = sum(counts) * 4 * BS^2 * D; bytes_min = Q + K + V read once and O "
+                                   "written once for the fused kernel (Q + K + V tiles read once for the tiled one)"},
+        "copy (calibration)": {"bytes_read": src.numel() * e, "bytes_written": dst.numel() * e},
+    }
+    if fused:
+        alg["bsa_fwd_kernel"]["bytes_min_fused"] = e * (2 * wl.lq + 2 * wl.lk) * H * D * B
+        alg["pool (Q)"] = {"bytes": e * H * D * B * wl.lq + e * H * D * g.nq_blk, "grid_blocks": g.nq_blk}
+        alg["pool (K)"] = {"bytes": e * H * D * B * wl.lk + e * H * D * g.nk_blk, "grid_blocks": g.nk_blk}
+    else:
+        alg["gather_pool_kernel<1> (Q)"] = {"bytes": e * H * D * B * (wl.lq + g.nq_blk * bs) + e * H * D * g.nq_blk}
+        alg["gather_pool_kernel<2> (K,V)"] = {"bytes": e * H * D * B * 2 * (wl.lk + g.nk_blk * bs)
+                                              + e * H * D * g.nk_blk}
+        alg["untile_kernel"] = {"bytes": e * H * D * B * 2 * wl.lq}
+    print(json.dumps({"profile": wl.name, "fused": fused, "launches_per_kernel": args.steps,
+                      "algorithmic_per_launch": alg}), flush=True)
 
 
 def cpu_baseline(wl, q, k, v, counts, ind, g, n_heads, flops, min_seconds=10.0):

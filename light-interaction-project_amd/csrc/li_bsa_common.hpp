@@ -134,12 +134,6 @@ __device__ __forceinline__ void dma16_sel(uint32_t mask, int bit, const void* sa
 __device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Token of tile row f of block blk in a grid of T frames; valid = inside.
-// x / d for x, d < 2^16 from magic = ceil(2^32 / d) (0 encodes d = 1).
-// Branch-free: umulhi(x, 0) = 0, and the identity term is x only for magic 0.
-__device__ __forceinline__ uint32_t udiv16(uint32_t x, uint32_t magic) {
-  return __umulhi(x, magic) | (x & (0u - (uint32_t)(magic == 0u)));
-}
-
 __device__ __forceinline__ int32_t tile_token(const BsaGather& g, int32_t T, uint32_t blk, uint32_t f, bool& valid) {
   const uint32_t ct = udiv16(blk, g.mg_nhnw), rem = blk - ct * (uint32_t)(g.nh * g.nw);
   const uint32_t ch = udiv16(rem, g.mg_nw), cw = rem - ch * (uint32_t)g.nw;

@@ -811,13 +811,10 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     };
     // M phase; group 0 (load = true) also issues the stage DMAs, group 1
     // runs the same MFMAs and reads without them.  Each is one basic block.
-    auto m_phase = [&](const char* vc, const char* kc, uint32_t vn, uint32_t kn, int bv, int bk,
+    // vb / kb: load sources of the V and K blocks the phase fetches, worked
+    // out during the preceding softmax phase.
+    auto m_phase = [&](const char* vc, const char* kc, uint32_t vn, uint32_t kn, const Blk& vb, const Blk& kb,
                        bool load) LI_INLINE {
-      Blk vb{nullptr, nullptr, 0u}, kb{nullptr, nullptr, 0u};
-      if (load) {
-        vb = src_of(bv, true);
-        kb = src_of(bk, false);
-      }
       vec8 opb[LA];
 #pragma unroll
       for (int u = 0; u < LA; ++u) opb[u] = read_op(u, vc, kc);
@@ -830,15 +827,22 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       }
       sched_m_phase<NPV, NU, LA, false>();
     };
-    auto x_phase = [&](int blk) LI_INLINE {
+    // pre() runs at the head of either branch, where its scalar work can
+    // interleave with the softmax's vector work.
+    auto x_phase = [&](int blk, auto&& pre) LI_INLINE {
       if (valid(blk)) {
+        pre();
         softmax();
       } else {
+        pre();
 #pragma unroll
         for (int st = 0; st < C::PST; ++st) ppk[st] = u32x4{0u, 0u, 0u, 0u};
       }
     };
-    int id_c = block_id(0), id_n = block_id(1), id_nn = block_id(2);
+    // Block ids i+1 .. i+3 are kept ahead of block i, so the sources of the
+    // next M phase can be worked out before it starts.
+    int id_c = block_id(0), id_n = block_id(1), id_nn = block_id(2), id_n3 = block_id(3);
+    Blk dv{nullptr, nullptr, 0u}, dk{nullptr, nullptr, 0u};
     if (grp == 0) {
       const Blk vb0 = src_of(safe(id_c), true);
       const Blk kb0 = src_of(safe(id_c), false);
@@ -849,6 +853,8 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
         dma(n + LPW, vb0, kb0, a_vs0, a_ks1);
         dma(n + LPW, vb0, kb1, a_vs0, a_ks0);
       }
+      dv = src_of(safe(id_n), true);
+      dk = src_of(safe(id_nn), false);
       wait_vm0();
     }
     __syncthreads();
@@ -857,18 +863,26 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     // meet only after the loop.
     auto pair = [&](int i, const char* vc, const char* kc, uint32_t vn, uint32_t kn, bool load) LI_INLINE {
       barrier();
-      m_phase(vc, kc, vn, kn, safe(id_n), safe(id_nn), load);
+      m_phase(vc, kc, vn, kn, dv, dk, load);
       barrier();
-      if (i + 1 < count) x_phase(id_n);
-      if (load) wait_loads();
+      const int id_x = id_n;
       id_c = id_n;
       id_n = id_nn;
-      id_nn = block_id(i + 3);
+      id_nn = id_n3;
+      id_n3 = block_id(i + 4);
+      auto next_sources = [&]() LI_INLINE {
+        if (load) {
+          dv = src_of(safe(id_n), true);
+          dk = src_of(safe(id_nn), false);
+        }
+      };
+      if (i + 1 < count) x_phase(id_x, next_sources);
+      if (load) wait_loads();
     };
     auto run = [&](bool load) LI_INLINE {
       scores(ks1);
       if (!load) barrier();
-      x_phase(id_c);
+      x_phase(id_c, [] {});
       for (int i = 0; i < count; i += 2) {
         pair(i, vs0, ks0, a_vs1, a_ks1, load);
         if (i + 1 < count) pair(i + 1, vs1, ks1, a_vs0, a_ks0, load);
@@ -981,15 +995,16 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
 }
 
 // Combines the two halves of each split query tile: O = (O0 a0 + O1 a1) /
-// (l0 a0 + l1 a1) with a_i = 2^(m_i - max(m0, m1)); lse = max + log2(l).  One
-// workgroup per split tile, two threads per row (64 d each).
+// (l0 a0 + l1 a1) with a_i = 2^(m_i - max(m0, m1)); lse = max + log2(l).  Four
+// workgroups per split tile (32 rows each), eight threads per row (16 d each,
+// 64 contiguous bytes of each partial).
 template <typename E, bool G = false>
 __global__ __launch_bounds__(256) void bsa_merge_kernel(BsaArgs a) {
   constexpr int BS = 128, D = 128;
-  const int p = blockIdx.x;
+  const int p = blockIdx.x >> 2;
   const int tile = a.n_full + p;
   const int bh = tile / a.nqt, m = tile % a.nqt;
-  const int rt = threadIdx.x >> 1, dh = threadIdx.x & 1;
+  const int rt = (blockIdx.x & 3) * 32 + (threadIdx.x >> 3), dq = threadIdx.x & 7;
   const int r = m * BS + rt;
   if (r >= a.Lq) return;
   // Padding rows of the grid have no output token but do have an LSE.
@@ -998,9 +1013,9 @@ __global__ __launch_bounds__(256) void bsa_merge_kernel(BsaArgs a) {
     const int b = bh / a.NH, h = bh % a.NH;
     bool ok;
     const int32_t l = tile_token(a.g, a.g.Tq, m, rt, ok);
-    if (ok) orow = a.out + b * a.g.os[0] + h * a.g.os[1] + (int64_t)l * a.g.os[2] + 64 * dh;
+    if (ok) orow = a.out + b * a.g.os[0] + h * a.g.os[1] + (int64_t)l * a.g.os[2] + 16 * dq;
   } else {
-    orow = a.out + ((int64_t)bh * a.Lq + r) * D + 64 * dh;
+    orow = a.out + ((int64_t)bh * a.Lq + r) * D + 16 * dq;
   }
   const float* p0 = a.part + (int64_t)(2 * p) * BS * (D + 2);
   const float* p1 = p0 + BS * (D + 2);
@@ -1011,20 +1026,27 @@ __global__ __launch_bounds__(256) void bsa_merge_kernel(BsaArgs a) {
   const float a0 = none ? 0.0f : __builtin_amdgcn_exp2f(m0 - mm);
   const float a1 = none ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
   const float l = l0 * a0 + l1 * a1;
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  const f32x4* o0 = reinterpret_cast<const f32x4*>(p0 + rt * D + 64 * dh);
-  const f32x4* o1 = reinterpret_cast<const f32x4*>(p1 + rt * D + 64 * dh);
+  if (orow) {
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const f32x4* o0 = reinterpret_cast<const f32x4*>(p0 + rt * D + 16 * dq);
+    const f32x4* o1 = reinterpret_cast<const f32x4*>(p1 + rt * D + 16 * dq);
+    f32x4 x0[4], x1[4];
 #pragma unroll
-  for (int i = 0; i < 8 && orow; ++i) {
-    const f32x4 x0 = o0[2 * i], x1 = o1[2 * i], y0 = o0[2 * i + 1], y1 = o1[2 * i + 1];
-    u32x4 pk;
-    pk[0] = cvt_pk<E>((x0[0] * a0 + x1[0] * a1) * inv, (x0[1] * a0 + x1[1] * a1) * inv);
-    pk[1] = cvt_pk<E>((x0[2] * a0 + x1[2] * a1) * inv, (x0[3] * a0 + x1[3] * a1) * inv);
-    pk[2] = cvt_pk<E>((y0[0] * a0 + y1[0] * a1) * inv, (y0[1] * a0 + y1[1] * a1) * inv);
-    pk[3] = cvt_pk<E>((y0[2] * a0 + y1[2] * a1) * inv, (y0[3] * a0 + y1[3] * a1) * inv);
-    *reinterpret_cast<u32x4*>(orow + 8 * i) = pk;
+    for (int i = 0; i < 4; ++i) {
+      x0[i] = o0[i];
+      x1[i] = o1[i];
+    }
+    u32x4 pk[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pk[i >> 1][2 * (i & 1)] = cvt_pk<E>((x0[i][0] * a0 + x1[i][0] * a1) * inv, (x0[i][1] * a0 + x1[i][1] * a1) * inv);
+      pk[i >> 1][2 * (i & 1) + 1] =
+          cvt_pk<E>((x0[i][2] * a0 + x1[i][2] * a1) * inv, (x0[i][3] * a0 + x1[i][3] * a1) * inv);
+    }
+    *reinterpret_cast<u32x4*>(orow) = pk[0];
+    *reinterpret_cast<u32x4*>(orow + 8) = pk[1];
   }
-  if (a.lse && dh == 0 && r < a.Lq) a.lse[(int64_t)bh * a.Lq + r] = none ? -__builtin_inff() : mm + __builtin_log2f(l);
+  if (a.lse && dq == 0) a.lse[(int64_t)bh * a.Lq + r] = none ? -__builtin_inff() : mm + __builtin_log2f(l);
 }
 
 template <typename E>
@@ -1033,7 +1055,7 @@ int launch_bsa_gather(BsaArgs& a, int tiles, hipStream_t s) {
   clear_launch_error();
   hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, 128, true>), dim3(a.n_full + 2 * nsplit), dim3(DmaCfg<128>::NTHR), 0, s,
                      a);
-  if (nsplit > 0) hipLaunchKernelGGL((bsa_merge_kernel<E, true>), dim3(nsplit), dim3(256), 0, s, a);
+  if (nsplit > 0) hipLaunchKernelGGL((bsa_merge_kernel<E, true>), dim3(4 * nsplit), dim3(256), 0, s, a);
   return launch_status();
 }
 
@@ -1043,7 +1065,7 @@ int launch_bsa_dma(BsaArgs& a, int tiles, hipStream_t s) {
   clear_launch_error();
   hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, BS>), dim3(a.n_full + 2 * nsplit), dim3(DmaCfg<BS>::NTHR), 0, s, a);
   if constexpr (BS == 128) {
-    if (nsplit > 0) hipLaunchKernelGGL(bsa_merge_kernel<E>, dim3(nsplit), dim3(256), 0, s, a);
+    if (nsplit > 0) hipLaunchKernelGGL(bsa_merge_kernel<E>, dim3(4 * nsplit), dim3(256), 0, s, a);
   }
   return launch_status();
 }
@@ -1069,7 +1091,7 @@ int launch_w4(BsaArgs& a, int tiles, hipStream_t s) {
   const int nsplit = tiles - a.n_full;
   clear_launch_error();
   launch_bsa_w4(std::is_same<E, Bf16>::value ? LI_DTYPE_BF16 : LI_DTYPE_F16, a, a.n_full + 2 * nsplit, s);
-  if (nsplit > 0) hipLaunchKernelGGL(bsa_merge_kernel<E>, dim3(nsplit), dim3(256), 0, s, a);
+  if (nsplit > 0) hipLaunchKernelGGL(bsa_merge_kernel<E>, dim3(4 * nsplit), dim3(256), 0, s, a);
   return launch_status();
 }
 
@@ -1170,7 +1192,6 @@ extern "C" int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t 
 
 namespace {
 
-uint32_t magic16(int32_t d) { return d == 1 ? 0u : (uint32_t)(((1ull << 32) + (uint64_t)d - 1) / (uint64_t)d); }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

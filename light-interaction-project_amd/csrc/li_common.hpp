@@ -43,6 +43,18 @@ struct F16 {
 
 __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) { return uint32_t(lo) | (uint32_t(hi) << 16); }
 
+// x / d for x, d < 2^16 without a division: magic = ceil(2^32 / d), and 0
+// encodes d = 1.  With magic = (2^32 + e) / d, 0 <= e < d, the quotient
+// x * magic / 2^32 = x / d + x e / (d 2^32) exceeds x / d by less than 1 / d,
+// so its floor is exact.  Branch-free: umulhi(x, 0) = 0, and the identity term
+// is x only for magic 0.
+__device__ __forceinline__ uint32_t udiv16(uint32_t x, uint32_t magic) {
+  return __umulhi(x, magic) | (x & (0u - (uint32_t)(magic == 0u)));
+}
+inline uint32_t magic16(int32_t d) {
+  return d == 1 ? 0u : (uint32_t)(((1ull << 32) + (uint64_t)d - 1) / (uint64_t)d);
+}
+
 // Launch status: call clear_launch_error() right before a kernel launch and
 // launch_status() right after it, so an error left by an earlier, unrelated
 // runtime call is not attributed to this launch.  The text of a failed

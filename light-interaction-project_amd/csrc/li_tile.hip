@@ -33,6 +33,7 @@ struct GatherArgs {
   int32_t NH, bs;
   li_tile_geom g;
   int32_t vec_src, vec_dst;
+  uint32_t mg_tw, mg_th;  // udiv16 magics of tw and th
 };
 
 __device__ __forceinline__ u32x4 load8(const uint16_t* p, int64_t stride, bool vec) {
@@ -71,37 +72,53 @@ __global__ __launch_bounds__(256) void gather_pool_kernel(GatherArgs a) {
   const int ch = rem % g.nh, ct = rem / g.nh;
   const bool vs = a.vec_src != 0, vd = a.vec_dst != 0;
 
-  const uint16_t* sbase[NT];
-  uint16_t* dbase[NT];
+  // NT tensors gathered into tiles (the first one also pooled); NT = 0 pools
+  // tensor 0 without writing tiles.
+  constexpr int NS = NT > 0 ? NT : 1;
+  const uint16_t* sbase[NS];
+  uint16_t* dbase[NS];
 #pragma unroll
-  for (int n = 0; n < NT; ++n) {
+  for (int n = 0; n < NS; ++n) {
     sbase[n] = a.src[n] + b * a.ss[n][0] + h * a.ss[n][1] + (int64_t)(8 * c) * a.ss[n][3];
-    dbase[n] = a.dst[n] ? a.dst[n] + b * a.ds[n][0] + h * a.ds[n][1] + (blk + a.dst_off) * a.ds[n][2] +
-                              (int64_t)(8 * c) * a.ds[n][4]
-                        : nullptr;
+    dbase[n] = NT > 0 ? a.dst[n] + b * a.ds[n][0] + h * a.ds[n][1] + (blk + a.dst_off) * a.ds[n][2] +
+                            (int64_t)(8 * c) * a.ds[n][4]
+                      : nullptr;
   }
 
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
 
-  for (int f = g0; f < a.bs; f += NG) {
-    const int fw = f % g.tw, r = f / g.tw;
-    const int fh = r % g.th, ft = r / g.th;
-    const int t = ct * g.tt + ft, hh = ch * g.th + fh, w = cw * g.tw + fw;
-    const bool valid = (t < g.T) && (hh < g.H) && (w < g.W);
-    const int64_t l = (int64_t)t * g.H * g.W + (int64_t)hh * g.W + w;
+  // R rows per thread in flight: all loads of a batch are issued before its
+  // rows are stored and summed (in row order, so the sums are unchanged).
+  constexpr int R = 8;
+  for (int f0 = g0; f0 < a.bs; f0 += R * NG) {
+    u32x4 v[NS][R];
 #pragma unroll
-    for (int n = 0; n < NT; ++n) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (valid) v = load8(sbase[n] + l * a.ss[n][2], a.ss[n][3], vs);
-      if (dbase[n]) store8(dbase[n] + (int64_t)f * a.ds[n][3], a.ds[n][4], vd, v);
-      if (n == 0) {
+    for (int i = 0; i < R; ++i) {
+      const uint32_t f = f0 + i * NG;
+      const uint32_t r = udiv16(f, a.mg_tw), fw = f - r * (uint32_t)g.tw;
+      const uint32_t ft = udiv16(r, a.mg_th), fh = r - ft * (uint32_t)g.th;
+      const int t = ct * g.tt + (int)ft, hh = ch * g.th + (int)fh, w = cw * g.tw + (int)fw;
+      const bool valid = ((int)f < a.bs) && (t < g.T) && (hh < g.H) && (w < g.W);
+      const int64_t l = (int64_t)t * g.H * g.W + (int64_t)hh * g.W + w;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc[2 * i] = acc[2 * i] + E::to_f32(uint16_t(v[i] & 0xFFFFu));
-          acc[2 * i + 1] = acc[2 * i + 1] + E::to_f32(uint16_t(v[i] >> 16));
-        }
+      for (int n = 0; n < NS; ++n) {
+        v[n][i] = u32x4{0u, 0u, 0u, 0u};
+        if (valid) v[n][i] = load8(sbase[n] + l * a.ss[n][2], a.ss[n][3], vs);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int f = f0 + i * NG;
+      if (f >= a.bs) break;
+#pragma unroll
+      for (int n = 0; n < NS; ++n)
+        if constexpr (NT > 0) store8(dbase[n] + (int64_t)f * a.ds[n][3], a.ds[n][4], vd, v[n][i]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc[2 * e] = acc[2 * e] + E::to_f32(uint16_t(v[0][i][e] & 0xFFFFu));
+        acc[2 * e + 1] = acc[2 * e + 1] + E::to_f32(uint16_t(v[0][i][e] >> 16));
       }
     }
   }
@@ -188,9 +205,12 @@ int launch_gather(int dtype, int32_t B, int32_t NH, int32_t D, GatherArgs& a, co
   const int64_t nblk = num_blocks(geom);
   if (nblk == 0) return LI_OK;
   if (nblk > 0x7FFFFFFF || (int64_t)B * NH > 65535) return LI_ERR_SHAPE;
+  if ((int64_t)geom->tt * geom->th * geom->tw >= 65536) return LI_ERR_SHAPE;
   a.NH = NH;
   a.bs = geom->tt * geom->th * geom->tw;
   a.g = *geom;
+  a.mg_tw = magic16(geom->tw);
+  a.mg_th = magic16(geom->th);
   dim3 grid((unsigned)nblk, (unsigned)(B * NH));
   clear_launch_error();
   if (dtype == LI_DTYPE_BF16 && D == 128)
@@ -277,7 +297,7 @@ extern "C" int li_pool(int dtype, int32_t B, int32_t NH, int32_t D, const void* 
   a.pool_off = pool_off;
   a.vec_src = vec_ok(src, src_strides, 4);
   a.vec_dst = 0;
-  return launch_gather<1>(dtype, B, NH, D, a, geom, static_cast<hipStream_t>(stream));
+  return launch_gather<0>(dtype, B, NH, D, a, geom, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int li_untile(int dtype, int32_t B, int32_t NH, int32_t D, const void* src, const int64_t src_strides[5],
