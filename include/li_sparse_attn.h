@@ -196,9 +196,11 @@ int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int32_t
  *   lse (B, NH, nq_blk*BS) fp32 per tiled query row, or NULL.
  *   workspace as for li_bsa_fwd (same size function with Lq = nq_blk*BS).
  * Same results as li_q_prep + li_kv_prep + li_bsa_fwd + li_untile, bit for
- * bit.  Built for D = 128, BS = tt*th*tw = 128, tw and W multiples of 4
- * (LI_ERR_UNSUPPORTED otherwise).  No counterpart in the reference as one
- * call.
+ * bit.  Built for D = 128, BS = tt*th*tw = 128, tw and W multiples of 4, a
+ * grid at least one tile high and wide (H >= th, W >= tw) and K/V token
+ * strides of at least D (LI_ERR_UNSUPPORTED otherwise); the byte offset of a
+ * K/V row from its tile's first token must fit 32 bits (LI_ERR_SHAPE).  No
+ * counterpart in the reference as one call.
  */
 int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D,
                       const void* q, const int64_t q_strides[4],
