@@ -24,6 +24,8 @@ struct BsaGather {
   // ceil(2^32 / d) for d = nh*nw, nw, th*tw, tw (0 for d = 1): x / d ==
   // umulhi(x, magic) exactly for x, d < 2^16.
   uint32_t mg_nhnw, mg_nw, mg_thtw, mg_tw;
+  // ~0 where the matching divisor is 1, else 0 (the identity term of udiv16m).
+  uint32_t id_nhnw, id_nw;
 };
 
 // Kernel arguments of the attention forward (all pointers are device
@@ -112,26 +114,32 @@ __device__ __forceinline__ void dma16_imm(const void* sbase, uint32_t voff, uint
                "i"(imm)
                : "memory");
 }
-// dma16_imm from one of two sources chosen by bit `bit` of the wave-uniform
-// `mask`: (sa, va) when it is set, else (sb, vb).  Three scalar instructions
-// and one vector select; they also cover the M0-write hazard.
-__device__ __forceinline__ void dma16_sel(uint32_t mask, int bit, const void* sa, uint32_t va, const void* sb,
-                                          uint32_t vb, uint32_t m0_addr, int imm) {
+// The source (sa, va) when bit `bit` of the wave-uniform `mask` is set, else
+// (sb, vb): three scalar instructions and one vector select.  Not volatile,
+// so the scheduler may compute it well before the load that uses it.
+struct DmaSrc {
   const void* base;
-  uint64_t lm;
   uint32_t voff;
-  asm volatile(
-      "s_bitcmp1_b32 %[mask], %[bit]\n\t"
+};
+__device__ __forceinline__ DmaSrc dma_sel(uint32_t mask, int bit, const void* sa, uint32_t va, const void* sb,
+                                         uint32_t vb) {
+  DmaSrc r;
+  uint64_t lm;
+  asm("s_bitcmp1_b32 %[mask], %[bit]\n\t"
       "s_cselect_b64 %[base], %[sa], %[sb]\n\t"
       "s_cselect_b64 %[lm], -1, 0\n\t"
-      "v_cndmask_b32_e64 %[voff], %[vb], %[va], %[lm]\n\t"
-      "global_load_lds_dwordx4 %[voff], %[base] offset:%[imm]"
-      : [base] "=&s"(base), [lm] "=&s"(lm), [voff] "=&v"(voff)
-      : [mask] "s"(mask), [bit] "i"(bit), [sa] "s"(sa), [sb] "s"(sb), [va] "v"(va), [vb] "v"(vb),
-        "{m0}"(m0_addr), [imm] "i"(imm)
-      : "memory", "scc");
+      "v_cndmask_b32_e64 %[voff], %[vb], %[va], %[lm]"
+      : [base] "=&s"(r.base), [lm] "=&s"(lm), [voff] "=&v"(r.voff)
+      : [mask] "s"(mask), [bit] "i"(bit), [sa] "s"(sa), [sb] "s"(sb), [va] "v"(va), [vb] "v"(vb)
+      : "scc");
+  return r;
 }
 __device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// udiv16 with its identity mask (~0 for magic 0, else 0) passed in.
+__device__ __forceinline__ uint32_t udiv16m(uint32_t x, uint32_t magic, uint32_t id) {
+  return __umulhi(x, magic) | (x & id);
+}
 
 // Token of tile row f of block blk in a grid of T frames; valid = inside.
 __device__ __forceinline__ int32_t tile_token(const BsaGather& g, int32_t T, uint32_t blk, uint32_t f, bool& valid) {

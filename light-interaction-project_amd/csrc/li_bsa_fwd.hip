@@ -746,42 +746,75 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       }
       coords(lane & 31, lane_ft, lane_fh, lane_fw);
     }
-    auto src_of = [&](int blk, bool is_v) LI_INLINE {
-      Blk s_{nullptr, nullptr, 0u};
-      if constexpr (!G) {
-        s_.alt = reinterpret_cast<const char*>((is_v ? vhead : khead) + (int64_t)blk * BS * D) + gw * LPW * 1024;
-      } else {
-        // Straight-line scalar code: both sides of each choice are computed.
-        const bool txt = blk < a.g.ntxt;
-        const int32_t vbs = blk - a.g.ntxt;
-        const uint32_t vb = (uint32_t)(vbs > 0 ? vbs : 0);
-        const uint32_t ct = udiv16(vb, a.g.mg_nhnw), rem = vb - ct * (uint32_t)(a.g.nh * a.g.nw);
-        const uint32_t ch = udiv16(rem, a.g.mg_nw), cw = rem - ch * (uint32_t)a.g.nw;
+    // A key block's geometry, shared by its K and V loads: its first token
+    // and this wave's in-grid chunk mask (0 for text blocks).  A block is a
+    // K block in one M phase and the V block of the next, so each M phase
+    // works out one new geometry.
+    struct Geo {
+      int32_t blk, l0;
+      uint32_t mask;
+      bool txt;
+    };
+    auto geo_of = [&](int blk) LI_INLINE {
+      Geo g_{blk, 0, 0u, false};
+      if constexpr (G) {
+        // Straight-line scalar code: both sides of each choice are computed;
+        // the text test is skipped when there are no text blocks.
+        bool txt = false;
+        uint32_t vb = (uint32_t)blk;
+        if (a.g.ntxt > 0) {
+          txt = blk < a.g.ntxt;
+          const int32_t vbs = blk - a.g.ntxt;
+          vb = (uint32_t)(vbs > 0 ? vbs : 0);
+        }
+        const uint32_t ct = udiv16m(vb, a.g.mg_nhnw, a.g.id_nhnw), rem = vb - ct * (uint32_t)(a.g.nh * a.g.nw);
+        const uint32_t ch = udiv16m(rem, a.g.mg_nw, a.g.id_nw), cw = rem - ch * (uint32_t)a.g.nw;
         const uint32_t t0 = ct * a.g.tt, h0 = ch * a.g.th, w0 = cw * a.g.tw;
-        const int64_t l0 = (int64_t)((t0 * a.g.H + h0) * a.g.W + w0);
-        s_.vis = (is_v ? vis_v : vis_k) + l0 * 2 * (is_v ? a.g.vs[2] : a.g.ks[2]);
+        g_.l0 = (int32_t)((t0 * a.g.H + h0) * a.g.W + w0);
         const bool inside = (lane_ft < a.g.Tk - t0) & (lane_fh < a.g.H - h0) & (lane_fw < a.g.W - w0);
         const uint32_t in_grid = (uint32_t)__ballot(inside);
-        s_.mask = (in_grid >> (gw * LPW)) & (txt ? 0u : (1u << LPW) - 1u);
-        const char* tb = (is_v ? txt_v : txt_k) + (int64_t)blk * (BS * D * 2);
-        s_.alt = txt ? tb : zero_rows;
+        g_.mask = (in_grid >> (gw * LPW)) & (txt ? 0u : (1u << LPW) - 1u);
+        g_.txt = txt;
+      }
+      return g_;
+    };
+    // Byte strides between K / V tokens (below 2^32: the host bounds the
+    // largest row offset of a tile).
+    const uint32_t kst = G ? (uint32_t)(2 * a.g.ks[2]) : 0u, vst = G ? (uint32_t)(2 * a.g.vs[2]) : 0u;
+    auto blk_src = [&](const Geo& g_, bool is_v) LI_INLINE {
+      Blk s_{nullptr, nullptr, 0u};
+      if constexpr (!G) {
+        s_.alt = reinterpret_cast<const char*>((is_v ? vhead : khead) + (int64_t)g_.blk * BS * D) + gw * LPW * 1024;
+      } else {
+        s_.vis = (is_v ? vis_v : vis_k) + (uint64_t)(uint32_t)g_.l0 * (is_v ? vst : kst);
+        s_.mask = g_.mask;
+        const char* tb = (is_v ? txt_v : txt_k) + (int64_t)g_.blk * (BS * D * 2);
+        s_.alt = g_.txt ? tb : zero_rows;
       }
       return s_;
     };
     // Chunk n of a group-0 wave's share of a stage: n < LPW is V, else K.
-    auto dma = [&](int n, const Blk& sv, const Blk& sk, uint32_t vn, uint32_t kn) LI_INLINE {
+    // src_n gives its global source, issue_n loads it into the stage.
+    auto src_n = [&](int n, const Blk& sv, const Blk& sk) LI_INLINE {
+      const bool isv = n < LPW;
+      const int j = isv ? n : n - LPW;
+      const Blk& s_ = isv ? sv : sk;
+      const uint32_t lin = isv ? v_src : k_src;
+      const char* alt = j < 4 ? s_.alt : s_.alt + 4096;
+      if constexpr (!G)
+        return DmaSrc{alt, lin};
+      else
+        return dma_sel(s_.mask, j, s_.vis, isv ? vvo[j] : kvo[j], alt, lin);
+    };
+    auto issue_n = [&](int n, const DmaSrc& src, uint32_t vn, uint32_t kn) LI_INLINE {
       const bool isv = n < LPW;
       const int j = isv ? n : n - LPW;
       const int c = gw * LPW + j;
       const int imm = (j & 3) * 1024;
-      const Blk& s_ = isv ? sv : sk;
-      const uint32_t m0 = (isv ? vn + c * 1024 : kn + c * 1088) - imm;
-      const uint32_t lin = isv ? v_src : k_src;
-      const char* alt = j < 4 ? s_.alt : s_.alt + 4096;
-      if constexpr (!G)
-        dma16_imm(alt, lin, m0, imm);
-      else
-        dma16_sel(s_.mask, j, s_.vis, isv ? vvo[j] : kvo[j], alt, lin, m0, imm);
+      dma16_imm(src.base, src.voff, (isv ? vn + c * 1024 : kn + c * 1088) - imm, imm);
+    };
+    auto dma = [&](int n, const Blk& sv, const Blk& sk, uint32_t vn, uint32_t kn) LI_INLINE {
+      issue_n(n, src_n(n, sv, sk), vn, kn);
     };
     // A operand of MFMA u of an M phase: the V^T tile of P V step
     // (st, dt) = (u / NDT, u % NDT) for u < NPV, else the K tile of S step
@@ -818,12 +851,20 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       vec8 opb[LA];
 #pragma unroll
       for (int u = 0; u < LA; ++u) opb[u] = read_op(u, vc, kc);
+      // The source of each load is worked out one load ahead, off the path
+      // between the MFMAs.
+      DmaSrc nxt{nullptr, 0u};
+      if (load) nxt = src_n(0, vb, kb);
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
         const vec8 op = opb[u % LA];
         if (u + LA < NU) opb[u % LA] = read_op(u + LA, vc, kc);
         mfma_u(u, op);
-        if (load && (u & 1)) dma(u >> 1, vb, kb, vn, kn);
+        if (load && (u & 1)) {
+          const int n = u >> 1;
+          issue_n(n, nxt, vn, kn);
+          if (n + 1 < 2 * LPW) nxt = src_n(n + 1, vb, kb);
+        }
       }
       sched_m_phase<NPV, NU, LA, false>();
     };
@@ -842,19 +883,26 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     // Block ids i+1 .. i+3 are kept ahead of block i, so the sources of the
     // next M phase can be worked out before it starts.
     int id_c = block_id(0), id_n = block_id(1), id_nn = block_id(2), id_n3 = block_id(3);
+    // The next id to read, stepped along the row and held at its last entry
+    // (the same clamp as block_id), so a read costs no index arithmetic.
+    const int64_t ist = a.is[3];
+    const_i32* idp = irow_s + (int64_t)(count > 4 ? 4 : (count > 0 ? count - 1 : 0)) * ist;
     Blk dv{nullptr, nullptr, 0u}, dk{nullptr, nullptr, 0u};
+    Geo geo_k{0, 0, 0u, false};  // geometry of the K block of the next M phase
     if (grp == 0) {
-      const Blk vb0 = src_of(safe(id_c), true);
-      const Blk kb0 = src_of(safe(id_c), false);
-      const Blk kb1 = src_of(safe(id_n), false);
+      const Geo g0 = geo_of(safe(id_c)), g1 = geo_of(safe(id_n));
+      const Blk vb0 = blk_src(g0, true);
+      const Blk kb0 = blk_src(g0, false);
+      const Blk kb1 = blk_src(g1, false);
 #pragma unroll
       for (int n = 0; n < LPW; ++n) {
         dma(n, vb0, kb0, a_vs0, a_ks1);
         dma(n + LPW, vb0, kb0, a_vs0, a_ks1);
         dma(n + LPW, vb0, kb1, a_vs0, a_ks0);
       }
-      dv = src_of(safe(id_n), true);
-      dk = src_of(safe(id_nn), false);
+      geo_k = geo_of(safe(id_nn));
+      dv = blk_src(g1, true);
+      dk = blk_src(geo_k, false);
       wait_vm0();
     }
     __syncthreads();
@@ -869,11 +917,13 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       id_c = id_n;
       id_n = id_nn;
       id_nn = id_n3;
-      id_n3 = block_id(i + 4);
+      id_n3 = *idp;
+      idp = i + 5 < count ? idp + ist : idp;
       auto next_sources = [&]() LI_INLINE {
         if (load) {
-          dv = src_of(safe(id_n), true);
-          dk = src_of(safe(id_nn), false);
+          dv = blk_src(geo_k, true);
+          geo_k = geo_of(safe(id_nn));
+          dk = blk_src(geo_k, false);
         }
       };
       if (i + 1 < count) x_phase(id_x, next_sources);
@@ -1286,6 +1336,8 @@ extern "C" int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D, co
   g.mg_nw = magic16(gq.nw);
   g.mg_thtw = magic16(gq.th * gq.tw);
   g.mg_tw = magic16(gq.tw);
+  g.id_nhnw = gq.nh * gq.nw == 1 ? ~0u : 0u;
+  g.id_nw = gq.nw == 1 ? ~0u : 0u;
   a.n_full = (int32_t)tiles;
   a.part = nullptr;
   if (workspace && aligned16(workspace)) {
