@@ -145,9 +145,12 @@ def main():
     scale = 1.0 / math.sqrt(D)
     fused = _pipeline.uses_fused(qd, kd, vd, wl.tile, wl.latent_hw)
     o_tok = torch.empty_like(qd)
-    tiled_attn = lambda: _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs)  # noqa: E731
+    # The attention launches as the call makes them (ragged rows: longest tiles first).
+    balance = _pipeline.ragged(params)
+    tiled_attn = lambda: _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs, balance=balance)  # noqa: E731
     fused_attn = lambda: _core.bsa_forward_gather(  # noqa: E731
-        qd, kd, vd, None, None, 0, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw, ind, cnt, scale, o_tok)
+        qd, kd, vd, None, None, 0, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw, ind, cnt, scale, o_tok,
+        balance=balance)
     # The roofline kernel is the attention kernel the call launches.
     attn = fused_attn if fused else tiled_attn
 
@@ -259,6 +262,7 @@ def profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params
     src = torch.empty(1 << 27, dtype=torch.bfloat16, device=dev).fill_(1.0)   # 256 MiB
     dst = torch.empty_like(src)
     fused = _pipeline.uses_fused(qd, kd, vd, wl.tile, wl.latent_hw)
+    balance = _pipeline.ragged(params)
     q_pool = torch.empty_like(q_p)
     k_pool = torch.empty_like(k_p)
     for _ in range(args.steps):
@@ -270,13 +274,13 @@ def profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params
             _core.pool(kd, k_pool, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
             fast_generate_indices(q_pool, k_pool, 0, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), params, dev)
             _core.bsa_forward_gather(qd, kd, vd, None, None, 0, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh,
-                                     g.nw, ind, cnt, scale, o_tok)
-            _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs, out=out)
+                                     g.nw, ind, cnt, scale, o_tok, balance=balance)
+            _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs, out=out, balance=balance)
         else:
             _core.q_prep(qd, q_t, q_p, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
             _core.kv_prep(kd, vd, k_all, v_all, k_p, 0, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
             fast_generate_indices(q_p, k_p, 0, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), params, dev)
-            _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs, out=out)
+            _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs, out=out, balance=balance)
             _core.untile(out.view(B, H, g.nq_blk, bs, D), o_lin, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
         dst.copy_(src)
     torch.cuda.synchronize()

@@ -172,13 +172,20 @@ int li_block_mask(int dtype, int32_t B, int32_t NH, int32_t D,
  * combined by a second kernel on the same stream.  Without it (or when it is
  * smaller than required) every tile runs whole.  Results are the same up to
  * fp32 rounding of the combination.
+ *
+ * flags: 0, or LI_BSA_BALANCE for rows of unequal length (ragged budgets):
+ * with the workspace, a small kernel first sorts the query tiles by their
+ * kept-block counts and the tiles start longest first (no tail split then).
+ * It changes the order of work only; results are identical to flags = 0
+ * without a tail split.  Used by the D = 128 kernels; ignored for D = 64.
  */
+enum li_bsa_flags { LI_BSA_BALANCE = 1 };
 int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int32_t D,
                const void* q, const void* k, const void* v,
                const int32_t* block_indices, const int64_t idx_strides[4], int32_t n_cols,
                const int32_t* block_counts, const int64_t cnt_strides[3],
                float sm_scale, int32_t block_size,
-               void* out, float* lse, void* workspace, int64_t workspace_bytes, void* stream);
+               void* out, float* lse, void* workspace, int64_t workspace_bytes, int32_t flags, void* stream);
 
 /*
  * Block-sparse attention with the tile gather and untile fused into the
@@ -194,7 +201,7 @@ int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int32_t
  *     visual block vb has id num_txt_blk + vb.
  *   block_indices / block_counts as for li_bsa_fwd, over the q_geom tiles.
  *   lse (B, NH, nq_blk*BS) fp32 per tiled query row, or NULL.
- *   workspace as for li_bsa_fwd (same size function with Lq = nq_blk*BS).
+ *   workspace and flags as for li_bsa_fwd (same size function with Lq = nq_blk*BS).
  * Same results as li_q_prep + li_kv_prep + li_bsa_fwd + li_untile, bit for
  * bit.  Built for D = 128, BS = tt*th*tw = 128, tw and W multiples of 4, a
  * grid at least one tile high and wide (H >= th, W >= tw) and K/V token
@@ -211,12 +218,14 @@ int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D,
                       const int32_t* block_indices, const int64_t idx_strides[4], int32_t n_cols,
                       const int32_t* block_counts, const int64_t cnt_strides[3],
                       float sm_scale, void* out, const int64_t out_strides[4], float* lse,
-                      void* workspace, int64_t workspace_bytes, void* stream);
+                      void* workspace, int64_t workspace_bytes, int32_t flags, void* stream);
 
 /*
- * Workspace bytes li_bsa_fwd can use for these sizes on the current device
- * (0: no split applies).  Depends on the device's CU count.  No counterpart
- * in the reference (its Triton launch has no split).
+ * Workspace bytes li_bsa_fwd / li_bsa_fwd_gather can use for these sizes on
+ * the current device: room for the tail split's partials or for the tile
+ * order of LI_BSA_BALANCE, whichever is larger (0 for D != 128).  Depends on
+ * the device's CU count.  No counterpart in the reference (its Triton launch
+ * has neither).
  */
 int64_t li_bsa_fwd_workspace_size(int32_t B, int32_t NH, int32_t Lq, int32_t D, int32_t block_size);
 

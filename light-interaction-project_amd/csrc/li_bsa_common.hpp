@@ -48,9 +48,24 @@ struct BsaArgs {
   // writes unnormalised fp32 O and (m, l) rows to `part` for the merge kernel.
   int32_t n_full;
   float* part;
+  // Optional dispatch order of the whole tiles (a permutation of
+  // [0, n_full)): position p of the XCD-aware unit order runs tile order[p].
+  const int32_t* order;
   // Fused path only (kernel template flag); unused otherwise.
   BsaGather g;
 };
+
+// Whole tile of work unit `id` (< a.n_full): ids are dealt round-robin over
+// the 8 XCDs, so they are remapped to give each XCD a contiguous range of
+// positions; a.order, when given, names the tile at each position.
+__device__ __forceinline__ int unit_tile(const BsaArgs& a, int id) {
+  const int xcd = id & 7, slot = id >> 3;
+  const int per = a.n_full >> 3, rem = a.n_full & 7;
+  const int pos = xcd * per + (xcd < rem ? xcd : rem) + slot;
+  if (!a.order) return pos;
+  const int t = __builtin_amdgcn_readfirstlane(a.order[pos]);
+  return t < 0 ? 0 : (t >= a.n_full ? a.n_full - 1 : t);
+}
 
 // Launches the 4-wave D = 128, BS = 128 kernel for units [0, a.n_full) whole
 // tiles plus the split half-units (li_bsa_fwd_w4.hip).

@@ -447,9 +447,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   const int id = blockIdx.x;
   int tile, half = -1;
   if (id < a.n_full) {
-    const int xcd = id & 7, slot = id >> 3;
-    const int per = a.n_full >> 3, rem = a.n_full & 7;
-    tile = xcd * per + (xcd < rem ? xcd : rem) + slot;
+    tile = unit_tile(a, id);
   } else {
     tile = a.n_full + ((id - a.n_full) >> 1);
     half = (id - a.n_full) & 1;
@@ -1169,6 +1167,49 @@ int device_cus() {
   return cached[dev] > 0 ? cached[dev] : 0;
 }
 
+// Dispatch order for rows of unequal length: within each XCD's range of
+// positions (the ranges unit_tile uses), tiles sorted by kept-block count,
+// longest first, so every XCD starts its longest work first (longest
+// processing time first).  A counting sort over 1024 buckets of the count
+// (exact when n_cols < 1024); one workgroup per XCD range.  Any order gives
+// the same results: each tile is computed on its own.
+__global__ __launch_bounds__(1024) void bsa_order_kernel(BsaArgs a, int32_t* order) {
+  __shared__ int hist[1024];
+  const int tid = threadIdx.x, x = blockIdx.x;
+  const int tiles = a.n_full;
+  const int per = tiles >> 3, rem = tiles & 7;
+  const int start = x * per + (x < rem ? x : rem), len = per + (x < rem ? 1 : 0);
+  const int nc = a.n_cols > 0 ? a.n_cols : 1;
+  auto bucket = [&](int tile) {
+    const int bh = tile / a.nqt, m = tile % a.nqt;
+    const int b = bh / a.NH, h = bh % a.NH;
+    int c = a.cnt[b * a.cs[0] + h * a.cs[1] + (int64_t)m * a.cs[2]];
+    c = c < 0 ? 0 : (c > nc ? nc : c);
+    return nc < 1024 ? nc - c : (int)(((int64_t)(nc - c) * 1023) / nc);
+  };
+  hist[tid] = 0;
+  __syncthreads();
+  for (int t = tid; t < len; t += 1024) atomicAdd(&hist[bucket(start + t)], 1);
+  __syncthreads();
+  // Exclusive prefix sum of the bucket sizes (Hillis-Steele, 1024 entries).
+  const int own = hist[tid];
+  for (int d = 1; d < 1024; d <<= 1) {
+    __syncthreads();
+    const int add = tid >= d ? hist[tid - d] : 0;
+    __syncthreads();
+    hist[tid] += add;
+  }
+  __syncthreads();
+  const int incl = hist[tid];
+  __syncthreads();
+  hist[tid] = incl - own;
+  __syncthreads();
+  for (int t = tid; t < len; t += 1024) {
+    const int p = atomicAdd(&hist[bucket(start + t)], 1);
+    order[start + p] = start + t;
+  }
+}
+
 // Query tiles whose block lists are split in two.  With one 8-wave
 // workgroup per CU, `tiles` whole tiles take ceil(tiles / cus) rounds; when
 // the last round holds r <= cus/2 tiles, splitting those r tiles into 2r half
@@ -1181,22 +1222,54 @@ int64_t split_tiles(int64_t tiles, int cus) {
 
 constexpr int64_t kPartBytesPerTile = 2 * 128 * (128 + 2) * 4;
 
+int64_t order_bytes(int64_t tiles) { return (tiles * 4 + 15) & ~(int64_t)15; }
+
+// Workspace use of one call: with LI_BSA_BALANCE (D = 128 kernels) the tile
+// order, built by bsa_order_kernel and no tail split; otherwise the tail
+// split's partials (D = 128, BS = 128).  Returns the launch status of the
+// order kernel (LI_OK when none runs).
+int plan_units(BsaArgs& a, int64_t tiles, int32_t D, int32_t block_size, void* workspace, int64_t workspace_bytes,
+               int32_t flags, hipStream_t s) {
+  a.n_full = (int32_t)tiles;
+  a.part = nullptr;
+  a.order = nullptr;
+  if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0 || D != 128) return LI_OK;
+  if (flags & LI_BSA_BALANCE) {
+    if (workspace_bytes < order_bytes(tiles)) return LI_OK;
+    int32_t* order = static_cast<int32_t*>(workspace);
+    clear_launch_error();
+    hipLaunchKernelGGL(bsa_order_kernel, dim3(8), dim3(1024), 0, s, a, order);
+    const int st = launch_status();
+    if (st == LI_OK) a.order = order;
+    return st;
+  }
+  if (block_size != 128) return LI_OK;
+  const int64_t ns = split_tiles(tiles, device_cus());
+  if (ns > 0 && workspace_bytes >= ns * kPartBytesPerTile) {
+    a.n_full = (int32_t)(tiles - ns);
+    a.part = static_cast<float*>(workspace);
+  }
+  return LI_OK;
+}
+
 }  // namespace
 }  // namespace li
 
 using namespace li;
 
 extern "C" int64_t li_bsa_fwd_workspace_size(int32_t B, int32_t NH, int32_t Lq, int32_t D, int32_t block_size) {
-  if (B <= 0 || NH <= 0 || Lq <= 0 || D != 128 || block_size != 128) return 0;
+  if (B <= 0 || NH <= 0 || Lq <= 0 || D != 128 || block_size <= 0) return 0;
   const int64_t tiles = (int64_t)((Lq + block_size - 1) / block_size) * B * NH;
-  return split_tiles(tiles, device_cus()) * kPartBytesPerTile;
+  const int64_t split = block_size == 128 ? split_tiles(tiles, device_cus()) * kPartBytesPerTile : 0;
+  const int64_t ord = order_bytes(tiles);
+  return split > ord ? split : ord;
 }
 
 extern "C" int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int32_t D, const void* q,
                           const void* k, const void* v, const int32_t* block_indices, const int64_t idx_strides[4],
                           int32_t n_cols, const int32_t* block_counts, const int64_t cnt_strides[3], float sm_scale,
                           int32_t block_size, void* out, float* lse, void* workspace, int64_t workspace_bytes,
-                          void* stream) {
+                          int32_t flags, void* stream) {
   if (!q || !k || !v || !block_indices || !idx_strides || !block_counts || !cnt_strides || !out)
     return LI_ERR_INVALID_ARG;
   if (B <= 0 || NH <= 0 || Lq < 0 || Lk < 0 || D <= 0 || n_cols < 0 || block_size <= 0) return LI_ERR_INVALID_ARG;
@@ -1226,16 +1299,9 @@ extern "C" int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t 
   a.nqt = (int32_t)nqt;
   a.n_cols = n_cols;
   a.qk_scale = sm_scale * 1.44269504f;
-  a.n_full = (int32_t)tiles;
-  a.part = nullptr;
-  if (workspace && D == 128 && block_size == 128 && (reinterpret_cast<uintptr_t>(workspace) & 15u) == 0) {
-    const int64_t ns = split_tiles(tiles, device_cus());
-    if (ns > 0 && workspace_bytes >= ns * kPartBytesPerTile) {
-      a.n_full = (int32_t)(tiles - ns);
-      a.part = static_cast<float*>(workspace);
-    }
-  }
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int st = plan_units(a, tiles, D, block_size, workspace, workspace_bytes, flags, s);
+  if (st != LI_OK) return st;
   if (dtype == LI_DTYPE_BF16) return dispatch_bsa<Bf16>(a, block_size, D, (int)tiles, s);
   return dispatch_bsa<F16>(a, block_size, D, (int)tiles, s);
 }
@@ -1259,7 +1325,7 @@ extern "C" int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D, co
                                  const int32_t* block_indices, const int64_t idx_strides[4], int32_t n_cols,
                                  const int32_t* block_counts, const int64_t cnt_strides[3], float sm_scale, void* out,
                                  const int64_t out_strides[4], float* lse, void* workspace, int64_t workspace_bytes,
-                                 void* stream) {
+                                 int32_t flags, void* stream) {
   if (!q_strides || !k_strides || !v_strides || !out_strides || !q_geom || !k_geom || !block_indices ||
       !idx_strides || !block_counts || !cnt_strides)
     return LI_ERR_INVALID_ARG;
@@ -1338,16 +1404,9 @@ extern "C" int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D, co
   g.mg_tw = magic16(gq.tw);
   g.id_nhnw = gq.nh * gq.nw == 1 ? ~0u : 0u;
   g.id_nw = gq.nw == 1 ? ~0u : 0u;
-  a.n_full = (int32_t)tiles;
-  a.part = nullptr;
-  if (workspace && aligned16(workspace)) {
-    const int64_t ns = split_tiles(tiles, device_cus());
-    if (ns > 0 && workspace_bytes >= ns * kPartBytesPerTile) {
-      a.n_full = (int32_t)(tiles - ns);
-      a.part = static_cast<float*>(workspace);
-    }
-  }
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int st = plan_units(a, tiles, D, 128, workspace, workspace_bytes, flags, s);
+  if (st != LI_OK) return st;
   if (dtype == LI_DTYPE_BF16) return launch_bsa_gather<Bf16>(a, (int)tiles, s);
   return launch_bsa_gather<F16>(a, (int)tiles, s);
 }

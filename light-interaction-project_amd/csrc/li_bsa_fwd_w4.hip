@@ -59,9 +59,7 @@ __global__ __launch_bounds__(256) void bsa_fwd_w4_kernel(BsaArgs a) {
   const int id = blockIdx.x;
   int tile, half = -1;
   if (id < a.n_full) {
-    const int xcd = id & 7, slot = id >> 3;
-    const int per = a.n_full >> 3, rem = a.n_full & 7;
-    tile = xcd * per + (xcd < rem ? xcd : rem) + slot;
+    tile = unit_tile(a, id);
   } else {
     tile = a.n_full + ((id - a.n_full) >> 1);
     half = (id - a.n_full) & 1;

@@ -122,11 +122,12 @@ def fused_supported(D, tile, latent_hw):
 
 
 def bsa_forward_gather(q, k, v, k_txt, v_txt, num_txt_blk, T_q, T_k, H, W, tt, th, tw, nh, nw, indices, counts,
-                       sm_scale, out, return_lse=False, split=True):
+                       sm_scale, out, return_lse=False, split=True, balance=False):
     """Block-sparse attention reading Q/K/V in token order and writing ``out`` in token order (li_bsa_fwd_gather).
 
     q/out (B,NH,Lq,D) and k/v (B,NH,Lk,D) views with any strides the kernel accepts; k_txt/v_txt the
-    zero-padded (B,NH,num_txt_blk*BS,D) contiguous text keys/values or None.  No host sync.
+    zero-padded (B,NH,num_txt_blk*BS,D) contiguous text keys/values or None.  ``split`` and ``balance``
+    as for ``bsa_forward``.  No host sync.
     """
     dev = _device_check(q, k, v, out, indices, counts)
     _same_dtype(q, k, v, out)
@@ -147,7 +148,7 @@ def bsa_forward_gather(q, k, v, k_txt, v_txt, num_txt_blk, T_q, T_k, H, W, tt, t
     bs = tt * th * tw
     lse = torch.empty((B, NH, nq * bs), dtype=torch.float32, device=dev) if return_lse else None
     with torch.cuda.device(dev):
-        ws_bytes = int(lib.li_bsa_fwd_workspace_size(B, NH, nq * bs, D, bs)) if split else 0
+        ws_bytes = int(lib.li_bsa_fwd_workspace_size(B, NH, nq * bs, D, bs)) if (split or balance) else 0
     ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev) if ws_bytes > 0 else None
     gq, gk = TileGeom(T_q, H, W, tt, th, tw, nh, nw), TileGeom(T_k, H, W, tt, th, tw, nh, nw)
     st = lib.li_bsa_fwd_gather(dtype_code(q), B, NH, D, q.data_ptr(), i64_array(q.stride()), k.data_ptr(),
@@ -157,7 +158,8 @@ def bsa_forward_gather(q, k, v, k_txt, v_txt, num_txt_blk, T_q, T_k, H, W, tt, t
                                ctypes.byref(gk), indices.data_ptr(), i64_array(indices.stride()), indices.shape[3],
                                counts.data_ptr(), i64_array(counts.stride()), float(sm_scale), out.data_ptr(),
                                i64_array(out.stride()), lse.data_ptr() if lse is not None else None,
-                               ws.data_ptr() if ws is not None else None, ws_bytes, _stream(dev))
+                               ws.data_ptr() if ws is not None else None, ws_bytes,
+                               _lib.LI_BSA_BALANCE if balance else 0, _stream(dev))
     check("li_bsa_fwd_gather", st)
     return (out, lse) if return_lse else out
 
@@ -267,10 +269,12 @@ def block_mask(q_pool, k_pool, *, metric, budget_mode, ratio, nh, nw, num_txt_bl
     return indices, counts
 
 
-def bsa_forward(q, k, v, indices, counts, sm_scale, block_size, return_lse=False, out=None, split=True):
+def bsa_forward(q, k, v, indices, counts, sm_scale, block_size, return_lse=False, out=None, split=True,
+                balance=False):
     """Block-sparse attention over contiguous (B,H,L,D) tensors (see li_bsa_fwd); no host sync.
 
-    ``split=False`` runs every query tile whole (no tail split workspace).
+    ``split=False`` runs every query tile whole (no tail split workspace).  ``balance=True`` (rows of
+    unequal length) starts the query tiles longest first instead (LI_BSA_BALANCE; no tail split).
     """
     dev = _device_check(q, k, v, indices, counts)
     _same_dtype(q, k, v)
@@ -293,13 +297,14 @@ def bsa_forward(q, k, v, indices, counts, sm_scale, block_size, return_lse=False
     # Scratch for splitting the query tiles of a partial last round (through
     # torch's caching allocator; stream-ordered, so it may be freed on return).
     with torch.cuda.device(dev):
-        ws_bytes = int(lib.li_bsa_fwd_workspace_size(B, NH, Lq, D, int(block_size))) if split else 0
+        ws_bytes = int(lib.li_bsa_fwd_workspace_size(B, NH, Lq, D, int(block_size))) if (split or balance) else 0
     ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev) if ws_bytes > 0 else None
     st = lib.li_bsa_fwd(dtype_code(q), B, NH, Lq, Lk, D, q.data_ptr(), k.data_ptr(), v.data_ptr(),
                         indices.data_ptr(), i64_array(indices.stride()), indices.shape[3], counts.data_ptr(),
                         i64_array(counts.stride()), float(sm_scale), int(block_size), out.data_ptr(),
                         lse.data_ptr() if lse is not None else None,
-                        ws.data_ptr() if ws is not None else None, ws_bytes, _stream(dev))
+                        ws.data_ptr() if ws is not None else None, ws_bytes,
+                        _lib.LI_BSA_BALANCE if balance else 0, _stream(dev))
     if st == _lib.LI_ERR_K_LEN:
         raise ValueError(f"K Length ({Lk}) must be divisible by logical_block_size ({block_size})")
     check("li_bsa_fwd", st)

@@ -16,7 +16,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL below)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libli_sparse_attn.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 LI_OK = 0
 LI_ERR_INVALID_ARG = -1
@@ -36,6 +36,8 @@ LI_METRIC_DOT = 2
 
 LI_BUDGET_HISTORY = 0
 LI_BUDGET_TOTAL = 1
+
+LI_BSA_BALANCE = 1
 
 _i64p = ctypes.POINTER(ctypes.c_int64)
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -70,11 +72,11 @@ SIGNATURES = {
     "li_block_mask": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p,
                                      ctypes.POINTER(MaskParams), _vp, _vp, _vp, _vp]),
     "li_bsa_fwd": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i64p, _i32,
-                                  _vp, _i64p, ctypes.c_float, _i32, _vp, _vp, _vp, _i64, _vp]),
+                                  _vp, _i64p, ctypes.c_float, _i32, _vp, _vp, _vp, _i64, _i32, _vp]),
     "li_bsa_fwd_workspace_size": (ctypes.c_int64, [_i32, _i32, _i32, _i32, _i32]),
     "li_bsa_fwd_gather": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
                                          _i32, ctypes.POINTER(TileGeom), ctypes.POINTER(TileGeom), _vp, _i64p, _i32,
-                                         _vp, _i64p, ctypes.c_float, _vp, _i64p, _vp, _vp, _i64, _vp]),
+                                         _vp, _i64p, ctypes.c_float, _vp, _i64p, _vp, _vp, _i64, _i32, _vp]),
     "li_pool": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p, _i64,
                                ctypes.POINTER(TileGeom), _vp]),
 }

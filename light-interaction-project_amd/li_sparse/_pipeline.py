@@ -73,7 +73,12 @@ def uses_fused(q, k_vis, v_vis, tile, latent_hw):
     return _core.fused_supported(q.shape[3], tile, latent_hw) and _fusable(q, k_vis, v_vis)
 
 
-def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events):
+def ragged(sparse_params):
+    """Whether the rows have their own budgets (then the attention starts its longest tiles first)."""
+    return sparse_params.get("row_budget") is not None
+
+
+def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance):
     """Pools, block selection, then one kernel that gathers, attends and untiles."""
     B, NH, _, D = q.shape
     dev, dt = q.device, q.dtype
@@ -96,14 +101,15 @@ def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events
     _stage(events, "index_end")
     _stage(events, "attn_start")
     _core.bsa_forward_gather(q, k_vis, v_vis, kt, vt, g.num_txt_blk, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw,
-                             g.nh, g.nw, indices, counts, 1.0 / math.sqrt(D), o_out)
+                             g.nh, g.nw, indices, counts, 1.0 / math.sqrt(D), o_out, balance=balance)
     _stage(events, "attn_end")
     _stage(events, "untile_start")
     _stage(events, "untile_end")
     return o_out if o_out.dtype == out_dtype else o_out.to(out_dtype)
 
 
-def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, events=None, fused=True):
+def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, events=None, fused=True,
+                     balance=False):
     """One sparse-attention forward.
 
     q (B,H,Lq,D); k_txt/v_txt (B,H,N_txt,D) or None; k_vis/v_vis (B,H,Lk,D), any strides.
@@ -113,7 +119,8 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
     shape allows it (D = 128, 128-token tiles, tw and W multiples of 4, a grid
     at least one tile high and wide, token views with unit d stride);
     otherwise, or with ``fused=False``, the tiled sequence q_prep / kv_prep /
-    attention / untile.  Both give the same bits.
+    attention / untile.  Both give the same bits.  ``balance`` (rows with their own budgets) starts
+    the longest query tiles first.
     """
     out_dtype = q.dtype
     if q.dtype not in (torch.bfloat16, torch.float16):
@@ -125,7 +132,7 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
     B, NH, _, D = q.shape
     dev, dt = q.device, q.dtype
     if fused and uses_fused(q, k_vis, v_vis, tile, (g.H, g.W)):
-        return _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events)
+        return _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance)
     _stage(events, "alloc_start")
     q_tiled = torch.empty((B, NH, g.nq_blk, g.bs, D), device=dev, dtype=dt)
     q_pool = torch.empty((B, NH, g.nq_blk, D), device=dev, dtype=dt)
@@ -149,7 +156,7 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
     _stage(events, "index_end")
     _stage(events, "attn_start")
     o_flat = _core.bsa_forward(q_tiled.flatten(2, 3), k_all.flatten(2, 3), v_all.flatten(2, 3), indices, counts,
-                               1.0 / math.sqrt(D), g.bs)
+                               1.0 / math.sqrt(D), g.bs, balance=balance)
     _stage(events, "attn_end")
     _stage(events, "untile_start")
     o_out = torch.empty_like(q)

@@ -68,4 +68,5 @@ def run_sparse_attention(q, k_txt, v_txt, k_vis, v_vis, block_idx, latent_hw, sp
         return fast_generate_indices(q_pool, k_pool, text_len, grid_q, grid_k, dict(sparse_params, tile_size=tile),
                                      q.device)
 
-    return _pipeline.sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select)
+    return _pipeline.sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select,
+                                      balance=_pipeline.ragged(sparse_params))

@@ -53,4 +53,5 @@ def run_sparse_prefill_attention(q, k_txt, v_txt, k_vis, v_vis, block_idx, laten
         return generate_prefill_indices(q_pool, k_pool, text_len, grid_k, dict(sparse_params, tile_size=tile),
                                         q.device)
 
-    return _pipeline.sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select)
+    return _pipeline.sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select,
+                                      balance=_pipeline.ragged(sparse_params))

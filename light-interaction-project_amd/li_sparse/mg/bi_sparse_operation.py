@@ -40,7 +40,7 @@ def run_sparse_attention(q, k, v, text_len, block_idx, latent_hw, sparse_params)
         return generate_prefill_indices(q_pool, k_pool, tl, grid_k, dict(sparse_params, tile_size=tile), q.device)
 
     o = _pipeline.sparse_attention(q, k_txt, v_txt, k[:, :, text_len:], v[:, :, text_len:], latent_hw, tile,
-                                   select, events)
+                                   select, events, balance=_pipeline.ragged(sparse_params))
     if events is not None:
         torch.cuda.synchronize()
         t = lambda a, b: events[a].elapsed_time(events[b])  # noqa: E731

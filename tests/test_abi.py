@@ -39,16 +39,16 @@ def test_host_validation_needs_no_gpu():
     s4, s3 = _strides(1, 1, 1, 1), _strides(1, 1, 1)
     bsa = L.lib.li_bsa_fwd
     # K length not a multiple of the block size
-    assert bsa(0, 1, 1, 128, 200, 128, fake, fake, fake, fake, s4, 1, fake, s3, 1.0, 128, fake, None, None, 0, None) == L.LI_ERR_K_LEN
+    assert bsa(0, 1, 1, 128, 200, 128, fake, fake, fake, fake, s4, 1, fake, s3, 1.0, 128, fake, None, None, 0, 0, None) == L.LI_ERR_K_LEN
     # null pointers
-    assert bsa(0, 1, 1, 128, 256, 128, None, fake, fake, fake, s4, 1, fake, s3, 1.0, 128, fake, None, None, 0, None) == L.LI_ERR_INVALID_ARG
+    assert bsa(0, 1, 1, 128, 256, 128, None, fake, fake, fake, s4, 1, fake, s3, 1.0, 128, fake, None, None, 0, 0, None) == L.LI_ERR_INVALID_ARG
     # unsupported head dim / block size / dtype
-    assert bsa(0, 1, 1, 128, 256, 96, fake, fake, fake, fake, s4, 1, fake, s3, 1.0, 128, fake, None, None, 0, None) == L.LI_ERR_UNSUPPORTED
-    assert bsa(0, 1, 1, 128, 256, 128, fake, fake, fake, fake, s4, 1, fake, s3, 1.0, 32, fake, None, None, 0, None) == L.LI_ERR_UNSUPPORTED
-    assert bsa(7, 1, 1, 128, 256, 128, fake, fake, fake, fake, s4, 1, fake, s3, 1.0, 128, fake, None, None, 0, None) == L.LI_ERR_UNSUPPORTED
+    assert bsa(0, 1, 1, 128, 256, 96, fake, fake, fake, fake, s4, 1, fake, s3, 1.0, 128, fake, None, None, 0, 0, None) == L.LI_ERR_UNSUPPORTED
+    assert bsa(0, 1, 1, 128, 256, 128, fake, fake, fake, fake, s4, 1, fake, s3, 1.0, 32, fake, None, None, 0, 0, None) == L.LI_ERR_UNSUPPORTED
+    assert bsa(7, 1, 1, 128, 256, 128, fake, fake, fake, fake, s4, 1, fake, s3, 1.0, 128, fake, None, None, 0, 0, None) == L.LI_ERR_UNSUPPORTED
     # misaligned pointers
     odd = ctypes.c_void_p(18)
-    assert bsa(0, 1, 1, 128, 256, 128, odd, fake, fake, fake, s4, 1, fake, s3, 1.0, 128, fake, None, None, 0, None) == L.LI_ERR_INVALID_ARG
+    assert bsa(0, 1, 1, 128, 256, 128, odd, fake, fake, fake, s4, 1, fake, s3, 1.0, 128, fake, None, None, 0, 0, None) == L.LI_ERR_INVALID_ARG
     # tile geometry with a wrong nh
     g = L.TileGeom(2, 30, 52, 2, 8, 8, 3, 7)
     assert L.lib.li_q_prep(0, 1, 1, 128, fake, s4, fake, _strides(1, 1, 1, 1, 1), fake, s4, ctypes.byref(g),

@@ -111,7 +111,8 @@ def test_tail_split_matches_whole_tiles_and_oracle(dev, waves):
         cus = torch.cuda.get_device_properties(dev).multi_processor_count
     r = tiles % cus if tiles > cus else 0
     nsplit = r if 0 < r <= cus // 2 else 0
-    assert ws == nsplit * 2 * 128 * 130 * 4
+    # room for the split partials, or for the tile order of the balanced mode
+    assert ws == max(nsplit * 2 * 128 * 130 * 4, (tiles * 4 + 15) // 16 * 16)
     rng = np.random.default_rng(5)
     q, k, v = _inputs(41, B, H, Lq, Lk, D)
     ind, cnt = _random_lists(rng, B, H, nq, nkb, 7)
@@ -194,3 +195,27 @@ def test_longcat_entry_fp32_inputs_and_strided_indices(dev):
     assert out.dtype == torch.bfloat16
     o_ref, _ = oatt.bsa_forward(_f64(q), _f64(k), _f64(v), ind, cnt, 1.0 / math.sqrt(D), bs)
     assert np.abs(out.float().cpu().numpy() - o_ref).max() <= TOL
+
+
+def test_balanced_order_gives_the_same_bits(dev):
+    """LI_BSA_BALANCE only reorders the query tiles: the same bits as whole tiles in natural order."""
+    bs, D, B, H, nq, nkb = 128, 128, 2, 3, 37, 40
+    Lq, Lk = nq * bs - 5, nkb * bs
+    print(f"[gpu] bsa balanced order B={B} H={H} nq={nq} ragged 0..{nkb}", flush=True)
+    rng = np.random.default_rng(17)
+    q, k, v = _inputs(43, B, H, Lq, Lk, D)
+    ind, cnt = _random_lists(rng, B, H, nq, nkb, nkb)   # row lengths 0..40, empty rows included
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    ii, cc = torch.from_numpy(ind).to(dev), torch.from_numpy(cnt).to(dev)
+    scale = 1.0 / math.sqrt(D)
+    out_b, lse_b = _core.bsa_forward(qd, kd, vd, ii, cc, scale, bs, return_lse=True, balance=True)
+    out_w, lse_w = _core.bsa_forward(qd, kd, vd, ii, cc, scale, bs, return_lse=True, split=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out_b.view(torch.int16), out_w.view(torch.int16))
+    assert torch.equal(torch.isneginf(lse_b), torch.isneginf(lse_w))
+    fin = torch.isfinite(lse_w)
+    assert torch.equal(lse_b[fin], lse_w[fin])
+    o_ref, _ = oatt.bsa_forward(_f64(q), _f64(k), _f64(v), ind, cnt, scale, bs)
+    err = np.abs(out_b.float().cpu().numpy() - o_ref).max()
+    print(f"[gpu]   balanced vs oracle: max abs err {err:.3e}", flush=True)
+    assert err <= TOL

@@ -126,3 +126,33 @@ def test_fused_rejects_unsupported_shapes(dev):
     out = _pipeline.sparse_attention(q, None, None, k, v, hw, tile, _select(params, dev))
     torch.cuda.synchronize()
     assert out.shape == q.shape and torch.isfinite(out.float()).all()
+
+
+def test_fused_balanced_order_gives_the_same_bits(dev):
+    """The ragged-row order on the fused kernel: the same bits as whole tiles in natural order."""
+    B, H, D, hw, tile = 1, 4, 128, (30, 52), (2, 8, 8)
+    print("[gpu] fused balanced order, ragged budgets", flush=True)
+    q, k, v, _, _ = _qkv(9, B, H, 4 * 1560, 16 * 1560, D, "blhd")
+    q, k, v = q.to(dev), k.to(dev), v.to(dev)
+    g = _pipeline.geometry(hw, tile, q.shape[2], k.shape[2], 0)
+    q_pool = torch.empty((B, H, g.nq_blk, D), device=dev, dtype=q.dtype)
+    k_pool = torch.empty((B, H, g.nk_blk, D), device=dev, dtype=q.dtype)
+    _core.pool(q, q_pool, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    _core.pool(k, k_pool, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    budgets = (np.random.default_rng(3).permutation(np.linspace(4, g.nk_blk, g.nq_blk)).astype(np.int64)).tolist()
+    params = {"tile_size": tile, "topk_ratio": 0.1, "sim_metric": "scaled_dot_product", "force_diag": True,
+              "force_sink": True, "row_budget": budgets}
+    ind, cnt = fast_generate_indices(q_pool, k_pool, 0, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), params, dev)
+    scale = 1.0 / math.sqrt(D)
+    args = (q, k, v, None, None, 0, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw, ind, cnt, scale)
+    out_b, lse_b = _core.bsa_forward_gather(*args, torch.empty_like(q), return_lse=True, balance=True)
+    out_w, lse_w = _core.bsa_forward_gather(*args, torch.empty_like(q), return_lse=True, split=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out_b.view(torch.int16), out_w.view(torch.int16))
+    assert torch.equal(lse_b, lse_w)
+    # the pipeline takes the balanced order for ragged budgets and still matches the tiled sequence
+    sel = lambda qp, kp, tl, gq, gk: fast_generate_indices(qp, kp, tl, gq, gk, params, dev)  # noqa: E731
+    o_f = _pipeline.sparse_attention(q, None, None, k, v, hw, tile, sel, balance=True)
+    o_t = _pipeline.sparse_attention(q, None, None, k, v, hw, tile, sel, fused=False, balance=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o_f.view(torch.int16), o_t.view(torch.int16))
