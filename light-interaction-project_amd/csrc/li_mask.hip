@@ -81,7 +81,13 @@ __device__ __forceinline__ float norm_den(const float* x) {
 
 __device__ __forceinline__ int wave_count(bool pred) { return __popcll(__ballot(pred)); }
 
-template <typename E, int D>
+#define LI_MASK_INLINE __attribute__((always_inline))
+
+// KR > 0: nk <= 64 KR and contiguous pool rows; a lane keeps the keys of
+// blocks lane, lane + 64, ... in registers and computes their dot products
+// side by side (each still summed over d in order).  KR = 0: any nk, keys
+// in the wave's LDS slice.
+template <typename E, int D, int KR>
 __global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a, int waves) {
   extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
   const li_mask_params& p = a.p;
@@ -119,37 +125,115 @@ __global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a, int waves) 
                    a.ks[1] % 8 == 0 && a.ks[2] % 8 == 0;
   const uint16_t* kbase = a.kp + b * a.ks[0] + h * a.ks[1];
   uint16_t* srow = a.scores ? a.scores + ((int64_t)bh * p.nq + qb) * nk : nullptr;
-  int nf = 0;
-  for (int j0 = 0; j0 < nk; j0 += 64) {
-    const int j = j0 + lane;
-    bool f = false;
-    if (j < nk) {
-      float x[D];
-      load_row<E, D>(kbase + (int64_t)j * a.ks[2], a.ks[3], vec, x);
-      float dot = 0.0f;
-      if (cosine) {
-        const float den = norm_den<E, D>(x);
-#pragma unroll
-        for (int d = 0; d < D; ++d) dot = dot + qv[d] * E::to_f32(E::from_f32(x[d] / den));
-      } else {
-#pragma unroll
-        for (int d = 0; d < D; ++d) dot = dot + qv[d] * x[d];
-      }
-      uint16_t s = E::from_f32(dot);
-      if (p.metric == LI_METRIC_SCALED_DOT) s = E::from_f32(E::to_f32(s) * p.scale);
-      if (srow) srow[j] = s;
-      f = (p.n_recent > 0) && (j >= nk - p.n_recent);
-      if (p.force_diag && j == pos) f = true;
-      if (p.force_sink && j == qb % hw) f = true;
-      if (p.force_neighbors && pos >= 0 && pos < nk) {
-        const int jt = j / hw, jh = (j % hw) / p.nw, jw = j % p.nw;
-        if (abs(jt - pt) + abs(jh - ph) + abs(jw - pw) <= 1) f = true;
-      }
-      keys[j] = f ? 0u : ((order16(s) << 16) | (0xFFFFu - (uint32_t)j));
+  // Score bits of block j -> forced flag and order key.
+  auto finish = [&](int j, float dot, bool& f) {
+    uint16_t s = E::from_f32(dot);
+    if (p.metric == LI_METRIC_SCALED_DOT) s = E::from_f32(E::to_f32(s) * p.scale);
+    if (srow) srow[j] = s;
+    f = (p.n_recent > 0) && (j >= nk - p.n_recent);
+    if (p.force_diag && j == pos) f = true;
+    if (p.force_sink && j == qb % hw) f = true;
+    if (p.force_neighbors && pos >= 0 && pos < nk) {
+      const int jt = j / hw, jh = (j % hw) / p.nw, jw = j % p.nw;
+      if (abs(jt - pt) + abs(jh - ph) + abs(jw - pw) <= 1) f = true;
     }
-    nf += wave_count(f);
+    return f ? 0u : ((order16(s) << 16) | (0xFFFFu - (uint32_t)j));
+  };
+  int nf = 0;
+  uint32_t kr[KR > 0 ? KR : 1];
+  if constexpr (KR > 0) {
+    // Dot products of this lane's KR blocks, 8 dimensions at a time.
+    float dot[KR], den[KR];
+#pragma unroll
+    for (int r = 0; r < KR; ++r) {
+      dot[r] = 0.0f;
+      den[r] = 1.0f;
+    }
+    if (cosine) {
+      float ss[KR];
+#pragma unroll
+      for (int r = 0; r < KR; ++r) ss[r] = 0.0f;
+#pragma unroll
+      for (int c = 0; c < D / 8; ++c)
+#pragma unroll
+        for (int r = 0; r < KR; ++r) {
+          const int j = r * 64 + lane;
+          if (j < nk) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(kbase + (int64_t)j * a.ks[2] + 8 * c);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const float x = E::to_f32(uint16_t((w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu));
+              ss[r] = ss[r] + x * x;
+            }
+          }
+        }
+      const float eps = E::to_f32(E::from_f32(1e-12f));
+#pragma unroll
+      for (int r = 0; r < KR; ++r) {
+        const float nrm = E::to_f32(E::from_f32(__builtin_sqrtf(ss[r])));
+        den[r] = nrm > eps ? nrm : eps;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c) {
+      float q8[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) q8[i] = qv[8 * c + i];
+#pragma unroll
+      for (int r = 0; r < KR; ++r) {
+        const int j = r * 64 + lane;
+        if (j < nk) {
+          const u32x4 w = *reinterpret_cast<const u32x4*>(kbase + (int64_t)j * a.ks[2] + 8 * c);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            float x = E::to_f32(uint16_t((w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu));
+            if (cosine) x = E::to_f32(E::from_f32(x / den[r]));
+            dot[r] = dot[r] + q8[i] * x;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < KR; ++r) {
+      const int j = r * 64 + lane;
+      bool f = false;
+      kr[r] = 0u;
+      if (j < nk) kr[r] = finish(j, dot[r], f);
+      nf += wave_count(f);
+    }
+  } else {
+    for (int j0 = 0; j0 < nk; j0 += 64) {
+      const int j = j0 + lane;
+      bool f = false;
+      if (j < nk) {
+        float x[D];
+        load_row<E, D>(kbase + (int64_t)j * a.ks[2], a.ks[3], vec, x);
+        float dot = 0.0f;
+        if (cosine) {
+          const float den = norm_den<E, D>(x);
+#pragma unroll
+          for (int d = 0; d < D; ++d) dot = dot + qv[d] * E::to_f32(E::from_f32(x[d] / den));
+        } else {
+#pragma unroll
+          for (int d = 0; d < D; ++d) dot = dot + qv[d] * x[d];
+        }
+        keys[j] = finish(j, dot, f);
+      }
+      nf += wave_count(f);
+    }
   }
   __builtin_amdgcn_wave_barrier();
+  // Key of block r * 64 + lane (0 past nk: never selected, never counted).
+  auto key_at = [&](int r) LI_MASK_INLINE {
+    if constexpr (KR > 0) {
+      return kr[r];
+    } else {
+      const int j = r * 64 + lane;
+      return j < nk ? keys[j] : 0u;
+    }
+  };
+  const int nchunk = KR > 0 ? KR : (nk + 63) / 64;
+  constexpr int KUNROLL = KR > 0 ? KR : 1;
 
   // 3. budget.
   int k;
@@ -180,10 +264,8 @@ __global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a, int waves) 
     for (int bit = 31; bit >= 0; --bit) {
       const uint32_t cand = prefix | (1u << bit);
       int c = 0;
-      for (int j0 = 0; j0 < nk; j0 += 64) {
-        const int j = j0 + lane;
-        c += wave_count(j < nk && keys[j] >= cand);
-      }
+#pragma unroll KUNROLL
+      for (int r = 0; r < nchunk; ++r) c += wave_count(key_at(r) >= cand);
       if (c >= kk) prefix = cand;
     }
     thr = prefix;
@@ -195,11 +277,12 @@ __global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a, int waves) 
   const int ntxt = p.num_txt_blk;
   for (int i = lane; i < ntxt && i < p.kmax; i += 64) irow[i] = i;
   int base = ntxt;
-  for (int j0 = 0; j0 < nk; j0 += 64) {
-    const int j = j0 + lane;
+#pragma unroll KUNROLL
+  for (int r = 0; r < nchunk; ++r) {
+    const int j = r * 64 + lane;
     bool sel = false;
     if (j < nk) {
-      const uint32_t key = keys[j];
+      const uint32_t key = key_at(r);
       sel = key == 0u || (kk > 0 && key >= thr);
     }
     const uint64_t m = __ballot(sel);
@@ -245,7 +328,11 @@ extern "C" int li_block_mask(int dtype, int32_t B, int32_t NH, int32_t D, const 
   a.counts = counts;
   a.scores = static_cast<uint16_t*>(scores);
   a.NH = NH;
-  // Per-wave LDS slice: nk keys + the query row; up to 4 waves (rows) per workgroup.
+  // Per-wave LDS slice: nk keys (LDS path only) + the query row; up to 4
+  // waves (rows) per workgroup.
+  const bool vec_k = k_pool_strides[3] == 1 && (reinterpret_cast<uintptr_t>(k_pool) & 15u) == 0 &&
+                     k_pool_strides[0] % 8 == 0 && k_pool_strides[1] % 8 == 0 && k_pool_strides[2] % 8 == 0;
+  const int kr = !vec_k ? 0 : (p.nk <= 256 ? 4 : (p.nk <= 1024 ? 16 : 0));
   const size_t per_wave = ((size_t)p.nk + D) * 4;
   int waves = (int)(65536 / per_wave);
   waves = waves < 1 ? 1 : (waves > 4 ? 4 : waves);
@@ -254,15 +341,25 @@ extern "C" int li_block_mask(int dtype, int32_t B, int32_t NH, int32_t D, const 
   dim3 block((unsigned)(64 * waves));
   hipStream_t s = static_cast<hipStream_t>(stream);
   clear_launch_error();
+#define LI_MASK_LAUNCH(E_, D_)                                                                          \
+  do {                                                                                                  \
+    if (kr == 4)                                                                                        \
+      hipLaunchKernelGGL((block_mask_kernel<E_, D_, 4>), grid, block, lds, s, a, waves);              \
+    else if (kr == 16)                                                                                  \
+      hipLaunchKernelGGL((block_mask_kernel<E_, D_, 16>), grid, block, lds, s, a, waves);             \
+    else                                                                                                \
+      hipLaunchKernelGGL((block_mask_kernel<E_, D_, 0>), grid, block, lds, s, a, waves);              \
+  } while (0)
   if (dtype == LI_DTYPE_BF16 && D == 128)
-    hipLaunchKernelGGL((block_mask_kernel<Bf16, 128>), grid, block, lds, s, a, waves);
+    LI_MASK_LAUNCH(Bf16, 128);
   else if (dtype == LI_DTYPE_BF16 && D == 64)
-    hipLaunchKernelGGL((block_mask_kernel<Bf16, 64>), grid, block, lds, s, a, waves);
+    LI_MASK_LAUNCH(Bf16, 64);
   else if (dtype == LI_DTYPE_F16 && D == 128)
-    hipLaunchKernelGGL((block_mask_kernel<F16, 128>), grid, block, lds, s, a, waves);
+    LI_MASK_LAUNCH(F16, 128);
   else if (dtype == LI_DTYPE_F16 && D == 64)
-    hipLaunchKernelGGL((block_mask_kernel<F16, 64>), grid, block, lds, s, a, waves);
+    LI_MASK_LAUNCH(F16, 64);
   else
     return LI_ERR_UNSUPPORTED;
+#undef LI_MASK_LAUNCH
   return launch_status();
 }

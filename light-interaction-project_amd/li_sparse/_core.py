@@ -224,6 +224,39 @@ def row_budgets(nf, nk, mode, ratio, min_budget=7, row_budget=None):
     return out
 
 
+_MASK_PLANS = {}
+
+
+def _mask_plan(dev, nq, nk, nh, nw, num_txt_blk, n_recent, force_diag, force_sink, force_neighbors, budget_mode,
+               ratio, min_budget, row_budget):
+    """Row length and device copy of explicit row budgets for one mask configuration.
+
+    Both depend only on the configuration, so they are worked out once per configuration and device (the
+    decode and prefill calls repeat the same one every layer and step), which also keeps the host-to-device
+    copy of the budgets out of the steady state.
+    """
+    rb = None if row_budget is None else tuple(int(x) for x in np.asarray(row_budget).reshape(-1))
+    key = (str(dev), nq, nk, nh, nw, num_txt_blk, n_recent, force_diag, force_sink, force_neighbors, budget_mode,
+           ratio, min_budget, rb)
+    plan = _MASK_PLANS.get(key)
+    if plan is not None:
+        return plan
+    nf = forced_counts(nq, nk, nh, nw, n_recent, force_diag, force_sink, force_neighbors)
+    rb_dev = None
+    if rb is not None:
+        if len(rb) != nq:
+            raise ValueError(f"row_budget has {len(rb)} entries for {nq} query blocks")
+        rb_dev = torch.tensor(rb, dtype=torch.int32, device=dev)
+        k = row_budgets(nf, nk, budget_mode, ratio, min_budget, np.asarray(rb, dtype=np.int64))
+    else:
+        k = row_budgets(nf, nk, budget_mode, ratio, min_budget)
+    plan = (int(num_txt_blk + (k.max() if nq > 0 else 0)), rb_dev)
+    if len(_MASK_PLANS) >= 64:
+        _MASK_PLANS.clear()
+    _MASK_PLANS[key] = plan
+    return plan
+
+
 def block_mask(q_pool, k_pool, *, metric, budget_mode, ratio, nh, nw, num_txt_blk=0, n_recent=0,
                force_diag=False, force_sink=False, force_neighbors=False, min_budget=7, row_budget=None,
                return_scores=False):
@@ -239,17 +272,8 @@ def block_mask(q_pool, k_pool, *, metric, budget_mode, ratio, nh, nw, num_txt_bl
     if tuple(k_pool.shape[:2]) != (B, NH) or k_pool.shape[3] != D:
         raise ValueError(f"pool shapes differ: {tuple(q_pool.shape)} vs {tuple(k_pool.shape)}")
     metric_code = METRICS.get(metric, _lib.LI_METRIC_DOT)
-    nf = forced_counts(nq, nk, nh, nw, n_recent, force_diag, force_sink, force_neighbors)
-    rb_dev = None
-    if row_budget is not None:
-        rb = np.asarray(row_budget, dtype=np.int64).reshape(-1)
-        if rb.size != nq:
-            raise ValueError(f"row_budget has {rb.size} entries for {nq} query blocks")
-        rb_dev = torch.as_tensor(rb.astype(np.int32)).to(dev, non_blocking=False)
-        k = row_budgets(nf, nk, budget_mode, ratio, min_budget, rb)
-    else:
-        k = row_budgets(nf, nk, budget_mode, ratio, min_budget)
-    kmax = int(num_txt_blk + (k.max() if nq > 0 else 0))
+    kmax, rb_dev = _mask_plan(dev, nq, nk, nh, nw, num_txt_blk, n_recent, bool(force_diag), bool(force_sink),
+                              bool(force_neighbors), budget_mode, float(ratio), int(min_budget), row_budget)
     indices = torch.empty((B, NH, nq, kmax), dtype=torch.int32, device=dev)
     counts = torch.empty((B, NH, nq), dtype=torch.int32, device=dev)
     scores = torch.empty((B, NH, nq, nk), dtype=q_pool.dtype, device=dev) if return_scores else None
@@ -263,7 +287,6 @@ def block_mask(q_pool, k_pool, *, metric, budget_mode, ratio, nh, nw, num_txt_bl
                            k_pool.data_ptr(), i64_array(k_pool.stride()), ctypes.byref(p), indices.data_ptr(),
                            counts.data_ptr(), scores.data_ptr() if scores is not None else None, _stream(dev))
     check("li_block_mask", st)
-    # rb_dev may be released now: the caching allocator reuses it only in stream order.
     if return_scores:
         return indices, counts, scores
     return indices, counts

@@ -106,3 +106,34 @@ def test_five_d_input_and_ties(dev):
         free = [j for j in range(8) if not forced[r, j]]
         want = sorted(list(np.nonzero(forced[r])[0]) + free[:max(0, 7 - int(forced[r].sum()))])
         assert ind[0, 0, r].tolist() == want
+
+
+@pytest.mark.parametrize("metric", ["cosine", "scaled_dot_product", "dot"])
+@pytest.mark.parametrize("case", ["nk_above_register_path", "strided_pools"])
+def test_lds_key_path(dev, metric, case):
+    """More key blocks than the register path holds (nk > 1024), and pool views without a unit d stride."""
+    print(f"[gpu] mask LDS path {case} metric={metric}", flush=True)
+    rng = np.random.default_rng(sum(map(ord, metric + case)))
+    D = 128
+    if case == "nk_above_register_path":
+        nh, nw, nt_q, nt_k = 4, 7, 1, 40           # nk = 1120
+    else:
+        nh, nw, nt_q, nt_k = 3, 5, 2, 6            # nk = 90
+    nq, nk = nt_q * nh * nw, nt_k * nh * nw
+    gen = torch.Generator().manual_seed(int(rng.integers(1 << 30)))
+    qp = torch.randn(1, 2, nq, D, generator=gen).to(torch.bfloat16)
+    kp = torch.randn(1, 2, nk, D, generator=gen).to(torch.bfloat16)
+    qd, kd = qp.to(dev), kp.to(dev)
+    if case == "strided_pools":
+        kd = kd.transpose(2, 3).contiguous().transpose(2, 3)   # d stride nk: element-wise loads
+    geo = {"nq_blk": nq, "nk_blk": nk, "nh": nh, "nw": nw}
+    params = {"tile_size": (2, 8, 8), "topk_ratio": 0.2, "force_diag": True, "force_sink": True}
+    forced, kk = oracle_forced(geo, params, "decode")
+    oind, ocnt, oscore, _ = omask.build_indices(bits(qp), bits(kp), metric=metric, forced=forced, k=kk,
+                                                num_txt_blk=0)
+    ind, cnt, sc = _core.block_mask(qd, kd, metric=metric, budget_mode=_lib.LI_BUDGET_HISTORY, ratio=0.2, nh=nh,
+                                    nw=nw, force_diag=True, force_sink=True, return_scores=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(sc), oscore)
+    assert np.array_equal(cnt.cpu().numpy(), ocnt)
+    assert np.array_equal(ind.cpu().numpy(), oind)
