@@ -27,6 +27,10 @@ sys.path.insert(0, os.path.join(REPO, "light-interaction-project_amd"))
 sys.path.insert(0, REPO)
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA
+# The e4m3 path does half of its FLOPs (Q K^T) at the fp8 peak and half (P V)
+# at the bf16 peak: its MFMA-bound time is F/2/P8 + F/2/P16.
+PEAK_MIXED_TFLOPS = 1.0 / (0.5 / PEAK_FP8_TFLOPS + 0.5 / PEAK_BF16_TFLOPS)
 PEAK_HBM_GBS = 8000.0
 
 
@@ -143,7 +147,8 @@ def main():
     flops = float(counts.sum()) * 4.0 * bs * bs * D
     qf, kf, vf = q_t.flatten(2, 3), k_all.flatten(2, 3), v_all.flatten(2, 3)
     scale = 1.0 / math.sqrt(D)
-    fused = _pipeline.uses_fused(qd, kd, vd, wl.tile, wl.latent_hw)
+    fp8 = bool(params.get("qk_fp8", False))
+    fused = _pipeline.uses_fused(qd, kd, vd, wl.tile, wl.latent_hw) and not fp8
     o_tok = torch.empty_like(qd)
     # The attention launches as the call makes them (ragged rows: longest tiles first).
     balance = _pipeline.ragged(params)
@@ -153,6 +158,15 @@ def main():
         balance=balance)
     # The roofline kernel is the attention kernel the call launches.
     attn = fused_attn if fused else tiled_attn
+    if fp8:
+        q8 = torch.empty((B, H, g.nq_blk, bs, D), dtype=_core.FP8, device=dev)
+        qs = torch.empty((B, H, g.nq_blk), dtype=torch.float32, device=dev)
+        k8 = torch.empty((B, H, g.nk_blk, bs, D), dtype=_core.FP8, device=dev)
+        ks = torch.empty((B, H, g.nk_blk), dtype=torch.float32, device=dev)
+        _core.tile_prep_fp8(qd, q8, qs, None, 0, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+        _core.kv_prep_fp8(kd, vd, k8, ks, v_all, k_p, 0, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+        q8f, k8f = q8.flatten(2, 3), k8.flatten(2, 3)
+        attn = lambda: _core.bsa_forward_fp8(q8f, qs, k8f, ks, vf, ind, cnt, scale, bs, balance=balance)  # noqa
 
     if args.profile:
         profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params, ind, cnt, flops, dev)
@@ -164,12 +178,13 @@ def main():
     attn_ms = mean(attn_per)   # average launch duration (events on the launch stream)
     attn_tflops = flops / (attn_ms * 1e-3) / 1e12
     tiled_info = None
-    if fused:
+    if fused or fp8:
         tiled_attn()
         _, tiled_per = event_loop(tiled_attn, max(5, args.steps // 5), stream)
         tiled_ms = mean(tiled_per)
         tiled_info = {"ms": round(tiled_ms, 4), "tflops": round(flops / (tiled_ms * 1e-3) / 1e12, 2),
-                      "note": "the same attention on pre-gathered tiles (the unfused sequence's kernel)"}
+                      "note": "the bf16 attention on bf16 tiles of the same inputs and lists" if fp8 else
+                              "the same attention on pre-gathered tiles (the unfused sequence's kernel)"}
 
     # Dense comparators: torch SDPA (valid tokens) and this kernel with every block kept.
     sdpa = lambda: torch.nn.functional.scaled_dot_product_attention(qd, kd, vd)  # noqa: E731
@@ -192,7 +207,9 @@ def main():
         full_flops = float(B * H * g.nq_blk * g.nk_blk) * 4.0 * bs * bs * D
         dense["own_kernel_all_blocks_ms"] = round(full_ms, 4)
         dense["own_kernel_all_blocks_tflops"] = round(full_flops / (full_ms * 1e-3) / 1e12, 2)
-    if fused:
+    if fp8:
+        kname = "bsa_fwd_dma_kernel<bf16,128,e4m3>"
+    elif fused:
         kname = "bsa_fwd_dma_kernel<bf16,128,gather>"
     elif D == 128 and bs in (64, 128):
         kname = "bsa_fwd_dma_kernel<bf16,128>"
@@ -203,9 +220,14 @@ def main():
     # (fused); the tiled sequence also writes and re-reads the tiles and untiles.
     if fused:
         prep_bytes = 2.0 * (wl.lq + wl.lk) * H * D * B
+    elif fp8:
+        # Q, K read as bf16 and written as e4m3 tiles; V gathered; output untiled.
+        prep_bytes = (2.0 * (wl.lq + 2 * wl.lk) + 1.0 * (g.nq_blk + g.nk_blk) * bs + 2.0 * g.nk_blk * bs
+                      + 2.0 * (g.nq_blk * bs + wl.lq)) * H * D * B
     else:
         prep_bytes = 2.0 * (wl.lq + 2 * wl.lk) * H * D * B + 2.0 * (g.nq_blk + 2 * g.nk_blk) * bs * H * D * B
 
+    peak = PEAK_MIXED_TFLOPS if fp8 else PEAK_BF16_TFLOPS
     result = {
         "metric": "sparse-attn fwd ms/call + TFLOPS (% MFMA peak) at HY shape, 30% keep",
         "value": round(flops / (step_ms * 1e-3) / 1e12, 2),
@@ -217,7 +239,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "e4m3 Q K^T (fp32 accumulate) + bf16 P V" if fp8 else "bf16",
         "data": "synthetic (seeded smooth (t,h,w) field + 0.5*N(0,1), bf16, Q pre-scaled by 1/sqrt(D))",
         "config": {"workload": wl.note, "batch": B, "heads": H, "head_dim": D, "lq": wl.lq, "lk": wl.lk,
                    "tile": list(wl.tile), "keep_ratio": wl.ratio, "block_size": bs, "nq_blocks": g.nq_blk,
@@ -230,11 +252,13 @@ def main():
                              "tflops": round(attn_tflops, 2),
                              "pct_bf16_peak": round(100.0 * attn_tflops / PEAK_BF16_TFLOPS, 2),
                              "retained_gflop": round(flops / 1e9, 2)},
-        "attention_kernel_tiled": tiled_info,
+        ("attention_kernel_bf16" if fp8 else "attention_kernel_tiled"): tiled_info,
         "dense_comparator": dense,
         "roofline": {"bound": "mfma", "kernel": kname,
-                     "achieved": round(attn_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
+                     "achieved": round(attn_tflops, 2), "peak": round(peak, 1), "unit": "TFLOP/s",
+                     "frac": round(attn_tflops / peak, 4),
+                     "peak_note": ("half the FLOPs (Q K^T) at the 5.0 PFLOP/s fp8 peak, half (P V) at the "
+                                   "2.5 PFLOP/s bf16 peak") if fp8 else "dense bf16 MFMA peak",
                      "traffic": load_traffic(kname) if args.workload == "hy" else None,
                      "traffic_unit": "bytes per launch (HBM/MALL side, rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
         "fused_path": fused,

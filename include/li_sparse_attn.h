@@ -229,6 +229,66 @@ int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D,
  */
 int64_t li_bsa_fwd_workspace_size(int32_t B, int32_t NH, int32_t Lq, int32_t D, int32_t block_size);
 
+/*
+ * fp8 variant of the tiled path: Q and K as OCP e4m3 (float8_e4m3fn) codes
+ * with one fp32 scale per tile block, V bf16.  The reference has no fp8
+ * path; these mirror li_q_prep / li_kv_prep / li_bsa_fwd (HYAR:166-202,
+ * HYK:158-216) with the score product Q K^T taken on e4m3 codes.
+ *
+ * Quantization of one tile block x (BS x D values, padding rows included):
+ * amax = max |x|, scale = amax / 448, codes = e4m3(x * (448 / amax)) rounded
+ * to nearest even (both quotients correctly rounded fp32); scale 1 and zero
+ * codes for an all-zero block.  Finite inputs never give a NaN code.
+ *
+ * li_tile_prep_fp8: li_q_prep's gather (dtype = the 16-bit type of src) with
+ * the tiles written as codes: dst (B, NH, nblk, BS, D) bytes, unit d stride,
+ * other strides multiples of 8, 8-byte aligned; scales (B, NH, nblk) fp32 at
+ * block (blk + dst_off).  mean (optional, NULL allowed) is li_q_prep's pool
+ * of the unquantized values, bit for bit, at block (blk + pool_off).  Built
+ * for BS <= 128 (D = 128) or BS <= 256 (D = 64).  Zero-padded contiguous
+ * text blocks (B, NH, n*BS, D) are quantized with the trivial geometry
+ * T = n, H = 1, W = BS, tile (1, 1, BS).
+ */
+int li_tile_prep_fp8(int dtype, int32_t B, int32_t NH, int32_t D,
+                     const void* src, const int64_t src_strides[4],
+                     void* dst, const int64_t dst_strides[5],
+                     float* scales, const int64_t scale_strides[3],
+                     void* mean, const int64_t mean_strides[4],
+                     int64_t dst_off, int64_t pool_off,
+                     const li_tile_geom* geom, void* stream);
+
+/*
+ * li_kv_prep with K written as codes and scales (as li_tile_prep_fp8) and V
+ * gathered unchanged; the K pool is li_kv_prep's, bit for bit.
+ */
+int li_kv_prep_fp8(int dtype, int32_t B, int32_t NH, int32_t D,
+                   const void* k_src, const int64_t k_src_strides[4],
+                   const void* v_src, const int64_t v_src_strides[4],
+                   void* k_dst, const int64_t k_dst_strides[5],
+                   float* k_scales, const int64_t k_scale_strides[3],
+                   void* v_dst, const int64_t v_dst_strides[5],
+                   void* k_mean, const int64_t mean_strides[4],
+                   int64_t dst_off, int64_t pool_off,
+                   const li_tile_geom* geom, void* stream);
+
+/*
+ * li_bsa_fwd with e4m3 Q and K: S = (q_scale[tile] * k_scale[block]) *
+ * (Q8 K8^T) from the codes on the fp8 MFMA (fp32 accumulation), then the
+ * same online softmax, P V in bf16 and outputs as li_bsa_fwd.
+ *   q8 (B, NH, Lq, D) codes, contiguous; q_scale (B, NH, ceil(Lq/128)) fp32, contiguous
+ *   k8 (B, NH, Lk, D) codes, contiguous; k_scale (B, NH, Lk/128) fp32, contiguous
+ *   v (B, NH, Lk, D) bf16, contiguous; out (B, NH, Lq, D) bf16
+ * Built for D = 128, block_size = 128 (LI_ERR_UNSUPPORTED otherwise);
+ * workspace and flags as for li_bsa_fwd (same size function).
+ */
+int li_bsa_fwd_fp8(int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int32_t D,
+                   const void* q8, const float* q_scale, const void* k8, const float* k_scale,
+                   const void* v,
+                   const int32_t* block_indices, const int64_t idx_strides[4], int32_t n_cols,
+                   const int32_t* block_counts, const int64_t cnt_strides[3],
+                   float sm_scale, int32_t block_size,
+                   void* out, float* lse, void* workspace, int64_t workspace_bytes, int32_t flags, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,10 @@ struct BsaArgs {
   // Optional dispatch order of the whole tiles (a permutation of
   // [0, n_full)): position p of the XCD-aware unit order runs tile order[p].
   const int32_t* order;
+  // e4m3 kernel only: q and k hold e4m3 codes (1 byte per element) with one
+  // fp32 scale per 128-row tile, (B*NH, nqt) and (B*NH, nkb) contiguous.
+  const float* q_scale;
+  const float* k_scale;
   // Fused path only (kernel template flag); unused otherwise.
   BsaGather g;
 };
@@ -77,6 +81,15 @@ namespace {
 __device__ __forceinline__ int kperm(int i) { return (i & 0x13) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// 32x32x64 e4m3 MFMA (v_mfma_f32_32x32x64_f8f6f4 with unit scales): lane l
+// holds A row l % 32 and B column l % 32, each with the 32 bytes k =
+// 32 (l / 32) .. +31 of the 64-deep step; the accumulator layout is that of
+// the 32x32x16 16-bit MFMA.
+__device__ __forceinline__ f32x16 mfma_e4m3(i32x8 a, i32x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
 
 // Lambdas of the kernels are always inlined: an outlined one would pass the
 // accumulators through scratch memory.

@@ -396,44 +396,55 @@ struct DmaCfg {
 };
 
 // Scheduling pins of an M phase (one basic block): the operand reads of the
-// first LA MFMAs, then per MFMA u: the MFMA, the reads of MFMA u + LA (two
-// transposing reads for a P V step, one 16-byte read for an S step) and, when
-// the phase loads a stage, one DMA after every odd MFMA.
-template <int NPV, int U, int END>
+// first LA MFMAs, then per MFMA u: the MFMA and the reads of MFMA u + LA (two
+// transposing reads for a P V step, RS 16-byte reads for an S step).
+template <int NPV, int RS, int U, int END>
 __device__ __forceinline__ void sched_first_reads() {
   if constexpr (U < END) {
-    __builtin_amdgcn_sched_group_barrier(0x100, U < NPV ? 2 : 1, 0);
-    sched_first_reads<NPV, U + 1, END>();
+    __builtin_amdgcn_sched_group_barrier(0x100, U < NPV ? 2 : RS, 0);
+    sched_first_reads<NPV, RS, U + 1, END>();
   }
 }
-template <int NPV, int NU, int LA, bool LOADS, int U>
+template <int NPV, int RS, int NU, int LA, int U>
 __device__ __forceinline__ void sched_m_units() {
   if constexpr (U < NU) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if constexpr (U + LA < NU) __builtin_amdgcn_sched_group_barrier(0x100, U + LA < NPV ? 2 : 1, 0);
-    sched_m_units<NPV, NU, LA, LOADS, U + 1>();
+    if constexpr (U + LA < NU) __builtin_amdgcn_sched_group_barrier(0x100, U + LA < NPV ? 2 : RS, 0);
+    sched_m_units<NPV, RS, NU, LA, U + 1>();
   }
 }
-template <int NPV, int NU, int LA, bool LOADS>
+// RS: LDS reads per S MFMA (one 16-byte read for 16-bit K, two for e4m3).
+template <int NPV, int RS, int NU, int LA>
 __device__ __forceinline__ void sched_m_phase() {
-  sched_first_reads<NPV, 0, LA>();
-  sched_m_units<NPV, NU, LA, LOADS, 0>();
+  sched_first_reads<NPV, RS, 0, LA>();
+  sched_m_units<NPV, RS, NU, LA, 0>();
 }
 
-template <typename E, int BS, bool G = false>
+// F8: Q and K are e4m3 codes with one fp32 scale per tile (BsaArgs::q_scale,
+// k_scale) and S^T = K Q^T is taken with the 32x32x64 e4m3 MFMA (four per
+// block and wave instead of sixteen); the block's score scale
+// qk_scale * q_scale * k_scale[blk] enters the softmax, and P V stays in
+// 16-bit.  The e4m3 K stage has 128-byte rows with no padding: the 16-byte
+// granule g of row r sits at slot g ^ ((r >> 1) & 7), so the 16 rows a
+// 16-lane group reads (any 16 aligned rows) fall in 16 distinct bank windows.
+template <typename E, int BS, bool G = false, bool F8 = false>
 __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   using C = DmaCfg<BS>;
   static_assert(!G || BS == 128, "token-order addressing is built for 128-row tiles");
+  static_assert(!F8 || (BS == 128 && !G), "the e4m3 kernel is built for tiled 128-row blocks");
   constexpr int D = 128;
   typedef typename E::vec8 vec8;
   typedef __attribute__((address_space(3))) void lds_void;
+  constexpr int KSB = F8 ? BS * D : C::K_STAGE_BYTES;  // bytes of a K stage
   // Separate arrays per stage let the compiler see that a load into one stage
   // never aliases the reads of the other.
-  __shared__ __attribute__((aligned(16))) char ks0[C::K_STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) char ks1[C::K_STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char ks0[KSB];
+  __shared__ __attribute__((aligned(16))) char ks1[KSB];
   __shared__ __attribute__((aligned(16))) char vs0[C::V_STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char vs1[C::V_STAGE_BYTES];
-  static_assert(C::NQW / 2 * C::NDT * 16 * 64 * 4 <= C::K_STAGE_BYTES, "epilogue exchange must fit a K stage");
+  // The epilogue's O exchange goes to the K stages, or to the V stages for F8.
+  static_assert(F8 || C::NQW / 2 * C::NDT * 16 * 64 * 4 <= C::K_STAGE_BYTES, "epilogue exchange must fit a K stage");
+  static_assert(!F8 || C::NQW / 2 * C::NDT * 16 * 64 * 4 <= C::V_STAGE_BYTES, "epilogue exchange must fit a V stage");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qq = wave >> 1, kh = wave & 1;
@@ -456,9 +467,10 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   const int b = bh / a.NH, h = bh % a.NH;
 
   const uint16_t* qhead = a.q + (int64_t)bh * a.Lq * D;
-  const uint16_t* khead = a.k + (int64_t)bh * a.nkb * BS * D;
   const uint16_t* vhead = a.v + (int64_t)bh * a.nkb * BS * D;
   uint16_t* ohead = a.out + (int64_t)bh * a.Lq * D;
+  constexpr int KEB = F8 ? 1 : 2;  // bytes per K element
+  const char* kbytes = reinterpret_cast<const char*>(a.k) + (int64_t)bh * a.nkb * BS * D * KEB;
   const int32_t* irow = a.idx + b * a.is[0] + h * a.is[1] + (int64_t)m * a.is[2];
   int count = a.cnt[b * a.cs[0] + h * a.cs[1] + (int64_t)m * a.cs[2]];
   count = count < 0 ? 0 : (count > a.n_cols ? a.n_cols : count);
@@ -506,7 +518,24 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   }
 
   vec8 qf[C::DS];
-  {
+  // e4m3 Q^T fragments: lane holds query row l32 and bytes 64 s + 32 hl .. +31.
+  i32x8 qf8[2];
+  float qk_scale = a.qk_scale;
+  if constexpr (F8) {
+    const int r = row0 + 32 * qq + l32;
+    const char* qrow8 = reinterpret_cast<const char*>(a.q) + ((int64_t)bh * a.Lq + r) * D;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+      if (r < a.Lq) {
+        lo = *reinterpret_cast<const u32x4*>(qrow8 + 64 * s + 32 * hl);
+        hi = *reinterpret_cast<const u32x4*>(qrow8 + 64 * s + 32 * hl + 16);
+      }
+      qf8[s] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    }
+    typedef __attribute__((address_space(4))) const float const_f32;
+    qk_scale *= ((const_f32*)a.q_scale)[(int64_t)bh * a.nqt + m];
+  } else {
     const uint16_t* qrow = nullptr;
     if constexpr (G) {
       bool ok;
@@ -538,12 +567,25 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     v_src_vis = (uint32_t)(rp * a.g.vs[2] * 2) + 2u * (32 * (((lane & 15) >> 2) ^ rp) + 8 * (lane & 3));
   }
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  // e4m3 K: a 1 KiB chunk is 8 rows of 128 bytes; lane t fills slot t % 8 of
+  // row t / 8 with the row's granule (t % 8) ^ ((row >> 1) & 7), which for
+  // chunk c is (t % 8) ^ (t / 16) ^ 4 (c % 2).
+  uint32_t k8_src[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) k8_src[p] = (lane >> 3) * 128 + 16 * ((lane & 7) ^ (lane >> 4) ^ (4 * p));
 
   // K operand byte offsets: row R = KW*kh + kperm(l32) (+32 kt), granule 2s+hl.
   const int R = C::KW * kh + kperm(l32);
   const int rc = R & 3;
   const int k_base = (R >> 2) * 1088 + rc * 256 + 16 * (hl ^ (rc & 1));
   const int k_off[2] = {k_base + 32 * (rc >> 1), k_base + 32 * (1 ^ (rc >> 1))};
+  // e4m3 K operand of step s (64 deep): granules 4 s + 2 hl and +1 of row R
+  // (+32 kt rows = 4096 bytes).
+  int k8_off[2][2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) k8_off[s][e] = R * 128 + 16 * ((4 * s + 2 * hl + e) ^ ((R >> 1) & 7));
   // V^T operand byte offsets for the transposing reads, one per 32-wide d tile.
   const int t16 = lane & 15, g16 = lane >> 4;
   const int v_base = (C::KW * kh + 8 * hl + (t16 >> 2)) * 256 + 32 * (g16 & 1) + 8 * (t16 & 3);
@@ -557,14 +599,28 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[dt][r] = 0.0f;
   float mrow = -__builtin_inff(), lrow = 0.0f;
-  const float qk_scale = a.qk_scale;
+  // Score scale of the current block: qk_scale (times the tile's Q scale for
+  // F8); for F8 also times the block's K scale, set before each softmax.
+  const float qk_base = qk_scale;
 
   // Score tile S^T = K Q^T of one block (this wave's key half).
   f32x16 sacc[C::NKT];
+  auto read_k8 = [&](const char* kd, int s, int kt) LI_INLINE {
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(kd + k8_off[s][0] + 4096 * kt);
+    const u32x4 hi = *reinterpret_cast<const u32x4*>(kd + k8_off[s][1] + 4096 * kt);
+    return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  };
   auto scores = [&](const char* kd) LI_INLINE {
     f32x16 z;
 #pragma unroll
     for (int r = 0; r < 16; ++r) z[r] = 0.0f;
+    if constexpr (F8) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int kt = 0; kt < C::NKT; ++kt) sacc[kt] = mfma_e4m3(read_k8(kd, s, kt), qf8[s], s == 0 ? z : sacc[kt]);
+      return;
+    }
 #pragma unroll
     for (int s = 0; s < C::DS; ++s) {
 #pragma unroll
@@ -675,11 +731,13 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     // it adds nothing (for finite block-0 data) and needs no branch.
     const int grp = wave_s >> 2;
     const int gw = wave_s & 3;          // wave within group 0
-    constexpr int LPW = 2 * C::CPW;     // chunks of one block per group-0 wave
+    constexpr int LPW = 2 * C::CPW;     // chunks of one V block per group-0 wave
+    constexpr int KPW = F8 ? LPW / 2 : LPW;  // chunks of one K block per group-0 wave
+    constexpr int NL = LPW + KPW;       // loads per M phase and group-0 wave
     constexpr int NPV = C::PST * C::NDT;
-    constexpr int NU = NPV + C::DS * C::NKT;
+    constexpr int NU = NPV + (F8 ? 2 * C::NKT : C::DS * C::NKT);
     constexpr int LA = 4;
-    static_assert(4 * LPW <= NU, "an M phase issues one load per two MFMAs");
+    static_assert(NL <= NU, "an M phase issues at most one load per MFMA");
     auto barrier = [&]() LI_INLINE {
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_barrier();
@@ -692,9 +750,10 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     };
     auto lds_addr = [&](char* p) LI_INLINE { return (uint32_t)(uintptr_t)(lds_void*)p; };
     const uint32_t a_ks0 = lds_addr(ks0), a_ks1 = lds_addr(ks1), a_vs0 = lds_addr(vs0), a_vs1 = lds_addr(vs1);
-    // A group-0 wave loads chunks c = gw * LPW + j (j < LPW) of every K and
-    // V block: 1 KiB each, block rows 4c..4c+3.  Each load is one
-    // instruction: scalar base + lane offset + instruction offset
+    // A group-0 wave loads chunks c = gw * LPW + j (j < LPW) of every V and
+    // 16-bit K block (1 KiB each, block rows 4c..4c+3), and chunks
+    // c = gw * KPW + j (j < KPW, rows 8c..8c+7) of an e4m3 K block.  Each load
+    // is one instruction: scalar base + lane offset + instruction offset
     // (j & 3) * 1024.
     //
     // Tiled blocks, text blocks (contiguous in the padded text buffer) and
@@ -782,7 +841,8 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     auto blk_src = [&](const Geo& g_, bool is_v) LI_INLINE {
       Blk s_{nullptr, nullptr, 0u};
       if constexpr (!G) {
-        s_.alt = reinterpret_cast<const char*>((is_v ? vhead : khead) + (int64_t)g_.blk * BS * D) + gw * LPW * 1024;
+        s_.alt = is_v ? reinterpret_cast<const char*>(vhead + (int64_t)g_.blk * BS * D) + gw * LPW * 1024
+                      : kbytes + (int64_t)g_.blk * BS * D * KEB + gw * KPW * 1024;
       } else {
         s_.vis = (is_v ? vis_v : vis_k) + (uint64_t)(uint32_t)g_.l0 * (is_v ? vst : kst);
         s_.mask = g_.mask;
@@ -797,7 +857,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       const bool isv = n < LPW;
       const int j = isv ? n : n - LPW;
       const Blk& s_ = isv ? sv : sk;
-      const uint32_t lin = isv ? v_src : k_src;
+      const uint32_t lin = isv ? v_src : (F8 ? k8_src[j & 1] : k_src);
       const char* alt = j < 4 ? s_.alt : s_.alt + 4096;
       if constexpr (!G)
         return DmaSrc{alt, lin};
@@ -807,37 +867,51 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     auto issue_n = [&](int n, const DmaSrc& src, uint32_t vn, uint32_t kn) LI_INLINE {
       const bool isv = n < LPW;
       const int j = isv ? n : n - LPW;
-      const int c = gw * LPW + j;
+      const int c = gw * (isv ? LPW : KPW) + j;
       const int imm = (j & 3) * 1024;
-      dma16_imm(src.base, src.voff, (isv ? vn + c * 1024 : kn + c * 1088) - imm, imm);
+      dma16_imm(src.base, src.voff, (isv ? vn + c * 1024 : kn + c * (F8 ? 1024 : 1088)) - imm, imm);
     };
     auto dma = [&](int n, const Blk& sv, const Blk& sk, uint32_t vn, uint32_t kn) LI_INLINE {
       issue_n(n, src_n(n, sv, sk), vn, kn);
     };
     // A operand of MFMA u of an M phase: the V^T tile of P V step
     // (st, dt) = (u / NDT, u % NDT) for u < NPV, else the K tile of S step
-    // (s, kt) = ((u - NPV) / NKT, (u - NPV) % NKT).
+    // (s, kt) = ((u - NPV) / NKT, (u - NPV) % NKT).  An operand is 16 bytes
+    // (p), or 32 bytes (k) for an e4m3 S step.
+    struct Op {
+      vec8 p;
+      i32x8 k;
+    };
     auto read_op = [&](int u, const char* vc, const char* kc) LI_INLINE {
+      Op r;
       if (u < NPV) {
         const int st = u / C::NDT, dt = u % C::NDT, kt = st >> 1, ip = st & 1;
         const uint16_t* p = reinterpret_cast<const uint16_t*>(vc + v_off[dt] + (32 * kt + 16 * ip) * 256);
         const u32x2 lo = lds_read_tr(p), hi = lds_read_tr(p + 4 * 128);
-        return __builtin_bit_cast(vec8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        r.p = __builtin_bit_cast(vec8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        return r;
       }
       const int w = u - NPV, s = w / C::NKT, kt = w % C::NKT;
-      return __builtin_bit_cast(vec8,
-                                *reinterpret_cast<const u32x4*>(kc + k_off[s & 1] + 8704 * kt + 64 * (s >> 1)));
+      if constexpr (F8)
+        r.k = read_k8(kc, s, kt);
+      else
+        r.p = __builtin_bit_cast(vec8,
+                                 *reinterpret_cast<const u32x4*>(kc + k_off[s & 1] + 8704 * kt + 64 * (s >> 1)));
+      return r;
     };
     f32x16 zero16;
 #pragma unroll
     for (int r = 0; r < 16; ++r) zero16[r] = 0.0f;
-    auto mfma_u = [&](int u, const vec8& op) LI_INLINE {
+    auto mfma_u = [&](int u, const Op& op) LI_INLINE {
       if (u < NPV) {
         const int st = u / C::NDT, dt = u % C::NDT;
-        o[dt] = E::mfma32(op, __builtin_bit_cast(vec8, ppk[st]), o[dt]);
+        o[dt] = E::mfma32(op.p, __builtin_bit_cast(vec8, ppk[st]), o[dt]);
       } else {
         const int w = u - NPV, s = w / C::NKT, kt = w % C::NKT;
-        sacc[kt] = E::mfma32(op, qf[s], s == 0 ? zero16 : sacc[kt]);
+        if constexpr (F8)
+          sacc[kt] = mfma_e4m3(op.k, qf8[s], s == 0 ? zero16 : sacc[kt]);
+        else
+          sacc[kt] = E::mfma32(op.p, qf[s], s == 0 ? zero16 : sacc[kt]);
       }
     };
     // M phase; group 0 (load = true) also issues the stage DMAs, group 1
@@ -846,25 +920,26 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     // out during the preceding softmax phase.
     auto m_phase = [&](const char* vc, const char* kc, uint32_t vn, uint32_t kn, const Blk& vb, const Blk& kb,
                        bool load) LI_INLINE {
-      vec8 opb[LA];
+      Op opb[LA];
 #pragma unroll
       for (int u = 0; u < LA; ++u) opb[u] = read_op(u, vc, kc);
       // The source of each load is worked out one load ahead, off the path
-      // between the MFMAs.
+      // between the MFMAs.  The NL loads are spread evenly: load n follows
+      // MFMA u when floor(u NL / NU) = n < floor((u + 1) NL / NU).
       DmaSrc nxt{nullptr, 0u};
       if (load) nxt = src_n(0, vb, kb);
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
-        const vec8 op = opb[u % LA];
+        const Op op = opb[u % LA];
         if (u + LA < NU) opb[u % LA] = read_op(u + LA, vc, kc);
         mfma_u(u, op);
-        if (load && (u & 1)) {
-          const int n = u >> 1;
+        const int n = u * NL / NU;
+        if (load && (u + 1) * NL / NU > n) {
           issue_n(n, nxt, vn, kn);
-          if (n + 1 < 2 * LPW) nxt = src_n(n + 1, vb, kb);
+          if (n + 1 < NL) nxt = src_n(n + 1, vb, kb);
         }
       }
-      sched_m_phase<NPV, NU, LA, false>();
+      sched_m_phase<NPV, F8 ? 2 : 1, NU, LA>();
     };
     // pre() runs at the head of either branch, where its scalar work can
     // interleave with the softmax's vector work.
@@ -887,14 +962,24 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     const_i32* idp = irow_s + (int64_t)(count > 4 ? 4 : (count > 0 ? count - 1 : 0)) * ist;
     Blk dv{nullptr, nullptr, 0u}, dk{nullptr, nullptr, 0u};
     Geo geo_k{0, 0, 0u, false};  // geometry of the K block of the next M phase
+    // F8: K scales of blocks id_n and id_nn, read one pair ahead of their
+    // softmax through the scalar cache.
+    typedef __attribute__((address_space(4))) const float const_f32;
+    const_f32* ksc = (const_f32*)a.k_scale + (int64_t)bh * a.nkb;
+    float sk_n = 0.0f, sk_nn = 0.0f;
+    if constexpr (F8) {
+      sk_n = ksc[safe(id_n)];
+      sk_nn = ksc[safe(id_nn)];
+    }
     if (grp == 0) {
       const Geo g0 = geo_of(safe(id_c)), g1 = geo_of(safe(id_n));
       const Blk vb0 = blk_src(g0, true);
       const Blk kb0 = blk_src(g0, false);
       const Blk kb1 = blk_src(g1, false);
 #pragma unroll
-      for (int n = 0; n < LPW; ++n) {
-        dma(n, vb0, kb0, a_vs0, a_ks1);
+      for (int n = 0; n < LPW; ++n) dma(n, vb0, kb0, a_vs0, a_ks1);
+#pragma unroll
+      for (int n = 0; n < KPW; ++n) {
         dma(n + LPW, vb0, kb0, a_vs0, a_ks1);
         dma(n + LPW, vb0, kb1, a_vs0, a_ks0);
       }
@@ -917,6 +1002,11 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       id_nn = id_n3;
       id_n3 = *idp;
       idp = i + 5 < count ? idp + ist : idp;
+      if constexpr (F8) {
+        qk_scale = qk_base * sk_n;
+        sk_n = sk_nn;
+        sk_nn = ksc[safe(id_nn)];
+      }
       auto next_sources = [&]() LI_INLINE {
         if (load) {
           dv = blk_src(geo_k, true);
@@ -930,6 +1020,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     auto run = [&](bool load) LI_INLINE {
       scores(ks1);
       if (!load) barrier();
+      if constexpr (F8) qk_scale = qk_base * ksc[safe(id_c)];
       x_phase(id_c, [] {});
       for (int i = 0; i < count; i += 2) {
         pair(i, vs0, ks0, a_vs1, a_ks1, load);
@@ -945,7 +1036,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     // One wave per SIMD: plain double buffering, block i+1 loaded while
     // block i is computed.
     auto load_block = [&](int blk, char* kd, char* vd) LI_INLINE {
-      const char* kb = reinterpret_cast<const char*>(khead + (int64_t)blk * BS * D);
+      const char* kb = kbytes + (int64_t)blk * BS * D * 2;
       const char* vb = reinterpret_cast<const char*>(vhead + (int64_t)blk * BS * D);
 #pragma unroll
       for (int j = 0; j < C::CPW; ++j) {
@@ -978,9 +1069,9 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
 
   // Merge the two key halves (waves kh = 0 and kh = 1 of the same qq).
   lrow += __shfl_xor(lrow, 32);
-  float* xo = reinterpret_cast<float*>(qq < C::NQW / 2 || C::NQW == 1 ? ks0 : ks1) +
-              (qq % (C::NQW > 1 ? C::NQW / 2 : 1)) * (C::NDT * 16 * 64);
-  float* xm = reinterpret_cast<float*>(vs0) + qq * (2 * 64);
+  char* xo_st = F8 ? (qq < C::NQW / 2 || C::NQW == 1 ? vs0 : vs1) : (qq < C::NQW / 2 || C::NQW == 1 ? ks0 : ks1);
+  float* xo = reinterpret_cast<float*>(xo_st) + (qq % (C::NQW > 1 ? C::NQW / 2 : 1)) * (C::NDT * 16 * 64);
+  float* xm = reinterpret_cast<float*>(F8 ? ks0 : vs0) + qq * (2 * 64);
   if (kh == 1) {
 #pragma unroll
     for (int dt = 0; dt < C::NDT; ++dt)
@@ -1104,6 +1195,15 @@ int launch_bsa_gather(BsaArgs& a, int tiles, hipStream_t s) {
   hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, 128, true>), dim3(a.n_full + 2 * nsplit), dim3(DmaCfg<128>::NTHR), 0, s,
                      a);
   if (nsplit > 0) hipLaunchKernelGGL((bsa_merge_kernel<E, true>), dim3(4 * nsplit), dim3(256), 0, s, a);
+  return launch_status();
+}
+
+int launch_bsa_fp8(BsaArgs& a, int tiles, hipStream_t s) {
+  const int nsplit = tiles - a.n_full;
+  clear_launch_error();
+  hipLaunchKernelGGL((bsa_fwd_dma_kernel<Bf16, 128, false, true>), dim3(a.n_full + 2 * nsplit),
+                     dim3(DmaCfg<128>::NTHR), 0, s, a);
+  if (nsplit > 0) hipLaunchKernelGGL(bsa_merge_kernel<Bf16>, dim3(4 * nsplit), dim3(256), 0, s, a);
   return launch_status();
 }
 
@@ -1409,4 +1509,47 @@ extern "C" int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D, co
   if (st != LI_OK) return st;
   if (dtype == LI_DTYPE_BF16) return launch_bsa_gather<Bf16>(a, (int)tiles, s);
   return launch_bsa_gather<F16>(a, (int)tiles, s);
+}
+
+extern "C" int li_bsa_fwd_fp8(int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int32_t D, const void* q8,
+                              const float* q_scale, const void* k8, const float* k_scale, const void* v,
+                              const int32_t* block_indices, const int64_t idx_strides[4], int32_t n_cols,
+                              const int32_t* block_counts, const int64_t cnt_strides[3], float sm_scale,
+                              int32_t block_size, void* out, float* lse, void* workspace, int64_t workspace_bytes,
+                              int32_t flags, void* stream) {
+  if (!q8 || !q_scale || !k8 || !k_scale || !v || !block_indices || !idx_strides || !block_counts || !cnt_strides ||
+      !out)
+    return LI_ERR_INVALID_ARG;
+  if (B <= 0 || NH <= 0 || Lq < 0 || Lk < 0 || D <= 0 || n_cols < 0 || block_size <= 0) return LI_ERR_INVALID_ARG;
+  if (Lk % block_size != 0) return LI_ERR_K_LEN;
+  if (D != 128 || block_size != 128) return LI_ERR_UNSUPPORTED;
+  if (!aligned16(q8) || !aligned16(k8) || !aligned16(v) || !aligned16(out) ||
+      ((reinterpret_cast<uintptr_t>(q_scale) | reinterpret_cast<uintptr_t>(k_scale)) & 3u))
+    return LI_ERR_INVALID_ARG;
+  if (Lq == 0) return LI_OK;
+  const int64_t nqt = (Lq + block_size - 1) / block_size;
+  const int64_t tiles = nqt * B * NH;
+  if (tiles > 0x7FFFFFFF) return LI_ERR_SHAPE;
+  BsaArgs a = {};
+  a.q = static_cast<const uint16_t*>(q8);
+  a.k = static_cast<const uint16_t*>(k8);
+  a.v = static_cast<const uint16_t*>(v);
+  a.q_scale = q_scale;
+  a.k_scale = k_scale;
+  a.idx = block_indices;
+  for (int i = 0; i < 4; ++i) a.is[i] = idx_strides[i];
+  a.cnt = block_counts;
+  for (int i = 0; i < 3; ++i) a.cs[i] = cnt_strides[i];
+  a.out = static_cast<uint16_t*>(out);
+  a.lse = lse;
+  a.NH = NH;
+  a.Lq = Lq;
+  a.nkb = Lk / block_size;
+  a.nqt = (int32_t)nqt;
+  a.n_cols = n_cols;
+  a.qk_scale = sm_scale * 1.44269504f;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int st = plan_units(a, tiles, D, block_size, workspace, workspace_bytes, flags, s);
+  if (st != LI_OK) return st;
+  return launch_bsa_fp8(a, (int)tiles, s);
 }

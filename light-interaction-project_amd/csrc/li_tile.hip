@@ -34,6 +34,9 @@ struct GatherArgs {
   li_tile_geom g;
   int32_t vec_src, vec_dst;
   uint32_t mg_tw, mg_th;  // udiv16 magics of tw and th
+  // e4m3 output of tensor 0 (Q8 kernels): one fp32 scale per tile block.
+  float* scale;
+  int64_t scs[3];
 };
 
 __device__ __forceinline__ u32x4 load8(const uint16_t* p, int64_t stride, bool vec) {
@@ -140,6 +143,127 @@ __global__ __launch_bounds__(256) void gather_pool_kernel(GatherArgs a) {
   }
 }
 
+// The same gather with tensor 0 written as OCP e4m3 codes (1 byte per
+// element, rows of D bytes) plus one fp32 scale per tile block:
+// amax = max |x| over the block (padding rows are zeros), scale = amax / 448,
+// codes e4m3(x * (448 / amax)), both quotients correctly rounded in fp32;
+// scale 1 and zero codes for an all-zero block.  After scaling no finite
+// element exceeds 448 (1 + 2^-23), which rounds to 448, so v_cvt_pk_fp8_f32
+// (round to nearest even) never saturates or yields NaN.  Its mean pool (of
+// the unquantized values, written when a.mean is set) and tensor 1 (NT = 2,
+// copied unquantized) are as in gather_pool_kernel.  The whole block is held
+// in registers (BS <= 8 NG rows): loads, then the workgroup's amax, then the
+// stores.
+template <typename E, int D, int NT>
+__global__ __launch_bounds__(256) void gather_fp8_kernel(GatherArgs a) {
+  constexpr int CPR = D / 8;
+  constexpr int NG = 256 / CPR;
+  constexpr int R = 8;
+  __shared__ float red[NG][D];
+  __shared__ uint32_t wmax[4];
+
+  const int blk = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / a.NH, h = bh % a.NH;
+  const int tid = threadIdx.x;
+  const int c = tid % CPR, g0 = tid / CPR;
+  const li_tile_geom& g = a.g;
+  const int cw = blk % g.nw, rem = blk / g.nw;
+  const int ch = rem % g.nh, ct = rem / g.nh;
+  const bool vs = a.vec_src != 0, vd = a.vec_dst != 0;
+
+  const uint16_t* sbase[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n)
+    sbase[n] = a.src[n] + b * a.ss[n][0] + h * a.ss[n][1] + (int64_t)(8 * c) * a.ss[n][3];
+  uint8_t* d8 = reinterpret_cast<uint8_t*>(a.dst[0]) + b * a.ds[0][0] + h * a.ds[0][1] +
+                (blk + a.dst_off) * a.ds[0][2] + 8 * c;
+  uint16_t* d1 = NT > 1 ? a.dst[NT - 1] + b * a.ds[NT - 1][0] + h * a.ds[NT - 1][1] +
+                              (blk + a.dst_off) * a.ds[NT - 1][2] + (int64_t)(8 * c) * a.ds[NT - 1][4]
+                        : nullptr;
+
+  u32x4 v[NT][R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const uint32_t f = g0 + i * NG;
+    const uint32_t r = udiv16(f, a.mg_tw), fw = f - r * (uint32_t)g.tw;
+    const uint32_t ft = udiv16(r, a.mg_th), fh = r - ft * (uint32_t)g.th;
+    const int t = ct * g.tt + (int)ft, hh = ch * g.th + (int)fh, w = cw * g.tw + (int)fw;
+    const bool valid = ((int)f < a.bs) && (t < g.T) && (hh < g.H) && (w < g.W);
+    const int64_t l = (int64_t)t * g.H * g.W + (int64_t)hh * g.W + w;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      v[n][i] = u32x4{0u, 0u, 0u, 0u};
+      if (valid) v[n][i] = load8(sbase[n] + l * a.ss[n][2], a.ss[n][3], vs);
+    }
+  }
+
+  // Largest magnitude: for finite 16-bit floats the magnitude bits order as
+  // the values do.
+  uint32_t mb = 0;
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t x = v[0][i][e];
+      mb = __builtin_elementwise_max(mb, __builtin_elementwise_max(x & 0x7FFFu, (x >> 16) & 0x7FFFu));
+    }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mb = __builtin_elementwise_max(mb, (uint32_t)__shfl_xor((int)mb, o));
+  if ((tid & 63) == 0) wmax[tid >> 6] = mb;
+  __syncthreads();
+  mb = __builtin_elementwise_max(__builtin_elementwise_max(wmax[0], wmax[1]),
+                                 __builtin_elementwise_max(wmax[2], wmax[3]));
+  const float amax = E::to_f32((uint16_t)mb);
+  const bool zero = !(amax > 0.0f);
+  const float scale = zero ? 1.0f : amax / 448.0f;
+  const float inv = zero ? 1.0f : 448.0f / amax;
+  if (tid == 0) a.scale[b * a.scs[0] + h * a.scs[1] + (blk + a.dst_off) * a.scs[2]] = scale;
+
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int f = g0 + i * NG;
+    if (f >= a.bs) break;
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = E::to_f32(uint16_t(v[0][i][e] & 0xFFFFu));
+      x[2 * e + 1] = E::to_f32(uint16_t(v[0][i][e] >> 16));
+    }
+    u32x2 q;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      int w = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * p] * inv, x[4 * p + 1] * inv, 0, false);
+      w = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * p + 2] * inv, x[4 * p + 3] * inv, w, true);
+      q[p] = (uint32_t)w;
+    }
+    *reinterpret_cast<u32x2*>(d8 + (int64_t)f * a.ds[0][3]) = q;
+    if constexpr (NT > 1) store8(d1 + (int64_t)f * a.ds[NT - 1][3], a.ds[NT - 1][4], vd, v[NT - 1][i]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = acc[e] + x[e];
+  }
+
+  if (!a.mean) return;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) red[g0][8 * c + i] = acc[i];
+  __syncthreads();
+  if (tid < D) {
+    float s[NG];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) s[i] = red[i][tid];
+#pragma unroll
+    for (int stride = NG / 2; stride >= 1; stride /= 2) {
+#pragma unroll
+      for (int i = 0; i < stride; ++i) s[i] = s[i] + s[i + stride];
+    }
+    const float mean = s[0] / (float)a.bs;
+    a.mean[b * a.ms[0] + h * a.ms[1] + (blk + a.pool_off) * a.ms[2] + (int64_t)tid * a.ms[3]] = E::from_f32(mean);
+  }
+}
+
 struct UntileArgs {
   const uint16_t* src;
   int64_t ss[5];
@@ -196,7 +320,7 @@ int check_geom(const li_tile_geom* g) {
 
 int64_t num_blocks(const li_tile_geom* g) { return (int64_t)((g->T + g->tt - 1) / g->tt) * g->nh * g->nw; }
 
-template <int NT>
+template <int NT, bool Q8 = false>
 int launch_gather(int dtype, int32_t B, int32_t NH, int32_t D, GatherArgs& a, const li_tile_geom* geom,
                   hipStream_t stream) {
   if (B <= 0 || NH <= 0) return LI_ERR_INVALID_ARG;
@@ -212,6 +336,22 @@ int launch_gather(int dtype, int32_t B, int32_t NH, int32_t D, GatherArgs& a, co
   a.mg_tw = magic16(geom->tw);
   a.mg_th = magic16(geom->th);
   dim3 grid((unsigned)nblk, (unsigned)(B * NH));
+  if constexpr (Q8) {
+    // The block is held in registers: at most 8 rows per thread.
+    if (a.bs > 8 * (256 / (D / 8))) return LI_ERR_UNSUPPORTED;
+    clear_launch_error();
+    if (dtype == LI_DTYPE_BF16 && D == 128)
+      hipLaunchKernelGGL((gather_fp8_kernel<Bf16, 128, NT>), grid, dim3(256), 0, stream, a);
+    else if (dtype == LI_DTYPE_BF16 && D == 64)
+      hipLaunchKernelGGL((gather_fp8_kernel<Bf16, 64, NT>), grid, dim3(256), 0, stream, a);
+    else if (dtype == LI_DTYPE_F16 && D == 128)
+      hipLaunchKernelGGL((gather_fp8_kernel<F16, 128, NT>), grid, dim3(256), 0, stream, a);
+    else if (dtype == LI_DTYPE_F16 && D == 64)
+      hipLaunchKernelGGL((gather_fp8_kernel<F16, 64, NT>), grid, dim3(256), 0, stream, a);
+    else
+      return LI_ERR_UNSUPPORTED;
+    return launch_status();
+  }
   clear_launch_error();
   if (dtype == LI_DTYPE_BF16 && D == 128)
     hipLaunchKernelGGL((gather_pool_kernel<Bf16, 128, NT>), grid, dim3(256), 0, stream, a);
@@ -330,4 +470,73 @@ extern "C" int li_untile(int dtype, int32_t B, int32_t NH, int32_t D, const void
   else
     return LI_ERR_UNSUPPORTED;
   return launch_status();
+}
+
+namespace {
+
+// e4m3 tile rows: unit d stride, 8-byte aligned rows; one scale per block.
+bool fp8_dst_ok(const void* p, const int64_t st[5]) {
+  return p && (reinterpret_cast<uintptr_t>(p) & 7u) == 0 && st[4] == 1 && st[0] % 8 == 0 && st[1] % 8 == 0 &&
+         st[2] % 8 == 0 && st[3] % 8 == 0;
+}
+
+}  // namespace
+
+extern "C" int li_tile_prep_fp8(int dtype, int32_t B, int32_t NH, int32_t D, const void* src,
+                                const int64_t src_strides[4], void* dst, const int64_t dst_strides[5],
+                                float* scales, const int64_t scale_strides[3], void* mean,
+                                const int64_t mean_strides[4], int64_t dst_off, int64_t pool_off,
+                                const li_tile_geom* geom, void* stream) {
+  if (!src || !src_strides || !dst_strides || !scales || !scale_strides || (mean && !mean_strides))
+    return LI_ERR_INVALID_ARG;
+  if (dst_off < 0 || pool_off < 0 || !fp8_dst_ok(dst, dst_strides)) return LI_ERR_INVALID_ARG;
+  GatherArgs a = {};
+  a.src[0] = static_cast<const uint16_t*>(src);
+  a.dst[0] = static_cast<uint16_t*>(dst);
+  for (int i = 0; i < 4; ++i) a.ss[0][i] = src_strides[i];
+  for (int i = 0; i < 5; ++i) a.ds[0][i] = dst_strides[i];
+  a.mean = static_cast<uint16_t*>(mean);
+  if (mean)
+    for (int i = 0; i < 4; ++i) a.ms[i] = mean_strides[i];
+  a.scale = scales;
+  for (int i = 0; i < 3; ++i) a.scs[i] = scale_strides[i];
+  a.dst_off = dst_off;
+  a.pool_off = pool_off;
+  a.vec_src = vec_ok(src, src_strides, 4);
+  a.vec_dst = 1;
+  return launch_gather<1, true>(dtype, B, NH, D, a, geom, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int li_kv_prep_fp8(int dtype, int32_t B, int32_t NH, int32_t D, const void* k_src,
+                              const int64_t k_src_strides[4], const void* v_src, const int64_t v_src_strides[4],
+                              void* k_dst, const int64_t k_dst_strides[5], float* k_scales,
+                              const int64_t k_scale_strides[3], void* v_dst, const int64_t v_dst_strides[5],
+                              void* k_mean, const int64_t mean_strides[4], int64_t dst_off, int64_t pool_off,
+                              const li_tile_geom* geom, void* stream) {
+  if (!k_src || !v_src || !v_dst || !k_mean || !k_src_strides || !v_src_strides || !k_dst_strides ||
+      !v_dst_strides || !mean_strides || !k_scales || !k_scale_strides)
+    return LI_ERR_INVALID_ARG;
+  if (dst_off < 0 || pool_off < 0 || !fp8_dst_ok(k_dst, k_dst_strides)) return LI_ERR_INVALID_ARG;
+  GatherArgs a = {};
+  a.src[0] = static_cast<const uint16_t*>(k_src);
+  a.src[1] = static_cast<const uint16_t*>(v_src);
+  a.dst[0] = static_cast<uint16_t*>(k_dst);
+  a.dst[1] = static_cast<uint16_t*>(v_dst);
+  for (int i = 0; i < 4; ++i) {
+    a.ss[0][i] = k_src_strides[i];
+    a.ss[1][i] = v_src_strides[i];
+    a.ms[i] = mean_strides[i];
+  }
+  for (int i = 0; i < 5; ++i) {
+    a.ds[0][i] = k_dst_strides[i];
+    a.ds[1][i] = v_dst_strides[i];
+  }
+  a.mean = static_cast<uint16_t*>(k_mean);
+  a.scale = k_scales;
+  for (int i = 0; i < 3; ++i) a.scs[i] = k_scale_strides[i];
+  a.dst_off = dst_off;
+  a.pool_off = pool_off;
+  a.vec_src = vec_ok(k_src, k_src_strides, 4) && vec_ok(v_src, v_src_strides, 4);
+  a.vec_dst = vec_ok(v_dst, v_dst_strides, 5);
+  return launch_gather<2, true>(dtype, B, NH, D, a, geom, static_cast<hipStream_t>(stream));
 }

@@ -94,6 +94,73 @@ def kv_prep(k_src, v_src, k_dst, v_dst, k_mean, dst_off, pool_off, T, H, W, tt, 
     check("li_kv_prep", st)
 
 
+FP8 = torch.float8_e4m3fn
+
+
+def _fp8_tiles_check(name, t, B, NH, nblk, bs, D):
+    if t.dtype != FP8:
+        raise TypeError(f"{name} must be float8_e4m3fn, got {t.dtype}")
+    if t.dim() != 5 or tuple(t.shape[:2]) != (B, NH) or t.shape[2] < nblk or tuple(t.shape[3:]) != (bs, D):
+        raise ValueError(f"{name} shape {tuple(t.shape)} does not hold {nblk} tiles of ({bs}, {D})")
+
+
+def _scale_check(name, t, B, NH, nblk):
+    if t.dtype != torch.float32 or t.dim() != 3 or tuple(t.shape[:2]) != (B, NH) or t.shape[2] < nblk:
+        raise ValueError(f"{name} must be float32 (B, NH, >= {nblk}), got {t.dtype} {tuple(t.shape)}")
+
+
+def tile_prep_fp8(src, dst, scales, mean, dst_off, pool_off, T, H, W, tt, th, tw, nh, nw):
+    """Tile gather into e4m3 codes with one fp32 scale per block (+ optional mean pool) (see li_tile_prep_fp8).
+
+    dst (B, NH, nblk, BS, D) float8_e4m3fn and scales (B, NH, nblk) float32, written at block blk + dst_off;
+    mean (or None) as q_prep's pool, at block blk + pool_off.
+    """
+    dev = _device_check(src, dst, scales, *([mean] if mean is not None else []))
+    B, NH, L, D = src.shape
+    dtype_code(src)
+    nblk, bs = num_blocks(T, tt, nh, nw), tt * th * tw
+    if L < T * H * W:
+        raise ValueError(f"source length {L} < T*H*W = {T * H * W}")
+    _fp8_tiles_check("dst", dst, B, NH, nblk + dst_off, bs, D)
+    _scale_check("scales", scales, B, NH, nblk + dst_off)
+    if mean is not None:
+        _same_dtype(src, mean)
+        if tuple(mean.shape[:2]) != (B, NH) or mean.shape[2] < nblk + pool_off or mean.shape[3] != D:
+            raise ValueError(f"pool buffer shape {tuple(mean.shape)} does not hold {nblk}+{pool_off} rows of {D}")
+    g = TileGeom(T, H, W, tt, th, tw, nh, nw)
+    st = lib.li_tile_prep_fp8(dtype_code(src), B, NH, D, src.data_ptr(), i64_array(src.stride()), dst.data_ptr(),
+                              i64_array(dst.stride()), scales.data_ptr(), i64_array(scales.stride()),
+                              mean.data_ptr() if mean is not None else None,
+                              i64_array(mean.stride()) if mean is not None else None, int(dst_off), int(pool_off),
+                              ctypes.byref(g), _stream(dev))
+    check("li_tile_prep_fp8", st)
+
+
+def kv_prep_fp8(k_src, v_src, k_dst, k_scales, v_dst, k_mean, dst_off, pool_off, T, H, W, tt, th, tw, nh, nw):
+    """kv_prep with K written as e4m3 codes + per-block scales and V copied unchanged (see li_kv_prep_fp8)."""
+    dev = _device_check(k_src, v_src, k_dst, k_scales, v_dst, k_mean)
+    _same_dtype(k_src, v_src, v_dst, k_mean)
+    B, NH, L, D = k_src.shape
+    if tuple(v_src.shape) != tuple(k_src.shape):
+        raise ValueError(f"K/V source shapes differ: {tuple(k_src.shape)} vs {tuple(v_src.shape)}")
+    nblk, bs = num_blocks(T, tt, nh, nw), tt * th * tw
+    if L < T * H * W:
+        raise ValueError(f"source length {L} < T*H*W = {T * H * W}")
+    _fp8_tiles_check("k_dst", k_dst, B, NH, nblk + dst_off, bs, D)
+    _scale_check("k_scales", k_scales, B, NH, nblk + dst_off)
+    if v_dst.shape[:2] != (B, NH) or v_dst.shape[2] < nblk + dst_off or v_dst.shape[3:] != (bs, D):
+        raise ValueError(f"v_dst shape {tuple(v_dst.shape)} does not hold {nblk}+{dst_off} tiles of ({bs}, {D})")
+    if tuple(k_mean.shape[:2]) != (B, NH) or k_mean.shape[2] < nblk + pool_off or k_mean.shape[3] != D:
+        raise ValueError(f"pool buffer shape {tuple(k_mean.shape)} does not hold {nblk}+{pool_off} rows")
+    g = TileGeom(T, H, W, tt, th, tw, nh, nw)
+    st = lib.li_kv_prep_fp8(dtype_code(k_src), B, NH, D, k_src.data_ptr(), i64_array(k_src.stride()),
+                            v_src.data_ptr(), i64_array(v_src.stride()), k_dst.data_ptr(), i64_array(k_dst.stride()),
+                            k_scales.data_ptr(), i64_array(k_scales.stride()), v_dst.data_ptr(),
+                            i64_array(v_dst.stride()), k_mean.data_ptr(), i64_array(k_mean.stride()), int(dst_off),
+                            int(pool_off), ctypes.byref(g), _stream(dev))
+    check("li_kv_prep_fp8", st)
+
+
 def pool(src, mean, pool_off, T, H, W, tt, th, tw, nh, nw):
     """Tile mean pool without writing tiles (see li_pool); same values as q_prep / kv_prep."""
     dev = _device_check(src, mean)
@@ -331,4 +398,52 @@ def bsa_forward(q, k, v, indices, counts, sm_scale, block_size, return_lse=False
     if st == _lib.LI_ERR_K_LEN:
         raise ValueError(f"K Length ({Lk}) must be divisible by logical_block_size ({block_size})")
     check("li_bsa_fwd", st)
+    return (out, lse) if return_lse else out
+
+
+def bsa_forward_fp8(q8, q_scale, k8, k_scale, v, indices, counts, sm_scale, block_size=128, return_lse=False,
+                    out=None, split=True, balance=False):
+    """Block-sparse attention with e4m3 Q/K and per-block scales, bf16 V and output (see li_bsa_fwd_fp8).
+
+    q8 (B,H,Lq,D) / k8 (B,H,Lk,D) float8_e4m3fn, contiguous; q_scale (B,H,ceil(Lq/128)) and
+    k_scale (B,H,Lk/128) float32; v (B,H,Lk,D) bfloat16.  ``split`` / ``balance`` as for bsa_forward.
+    """
+    dev = _device_check(q8, q_scale, k8, k_scale, v, indices, counts)
+    if q8.dtype != FP8 or k8.dtype != FP8:
+        raise TypeError("q8 and k8 must be float8_e4m3fn")
+    if v.dtype != torch.bfloat16:
+        raise TypeError(f"v must be bfloat16, got {v.dtype}")
+    if not (q8.is_contiguous() and k8.is_contiguous() and v.is_contiguous() and q_scale.is_contiguous()
+            and k_scale.is_contiguous()):
+        raise ValueError("q8, k8, v and the scales must be contiguous")
+    B, NH, Lq, D = q8.shape
+    Lk = k8.shape[2]
+    if tuple(k8.shape) != (B, NH, Lk, D) or tuple(v.shape) != (B, NH, Lk, D):
+        raise ValueError(f"shape mismatch q {tuple(q8.shape)} k {tuple(k8.shape)} v {tuple(v.shape)}")
+    nqt = ceil_div(Lq, block_size)
+    if tuple(q_scale.shape) != (B, NH, nqt) or q_scale.dtype != torch.float32:
+        raise ValueError(f"q_scale must be float32 {(B, NH, nqt)}, got {q_scale.dtype} {tuple(q_scale.shape)}")
+    if Lk % block_size == 0 and (tuple(k_scale.shape) != (B, NH, Lk // block_size) or k_scale.dtype != torch.float32):
+        raise ValueError(f"k_scale must be float32 {(B, NH, Lk // block_size)}, got {tuple(k_scale.shape)}")
+    if indices.dtype != torch.int32 or counts.dtype != torch.int32:
+        raise TypeError("block indices and counts must be int32")
+    if indices.dim() != 4 or tuple(indices.shape[:2]) != (B, NH) or indices.shape[2] < nqt:
+        raise ValueError(f"block_indices shape {tuple(indices.shape)} does not cover {nqt} query tiles")
+    if counts.dim() != 3 or tuple(counts.shape[:2]) != (B, NH) or counts.shape[2] < nqt:
+        raise ValueError(f"block_counts shape {tuple(counts.shape)} does not cover {nqt} query tiles")
+    if out is None:
+        out = torch.empty((B, NH, Lq, D), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((B, NH, Lq), dtype=torch.float32, device=dev) if return_lse else None
+    with torch.cuda.device(dev):
+        ws_bytes = int(lib.li_bsa_fwd_workspace_size(B, NH, Lq, D, int(block_size))) if (split or balance) else 0
+    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev) if ws_bytes > 0 else None
+    st = lib.li_bsa_fwd_fp8(B, NH, Lq, Lk, D, q8.data_ptr(), q_scale.data_ptr(), k8.data_ptr(), k_scale.data_ptr(),
+                            v.data_ptr(), indices.data_ptr(), i64_array(indices.stride()), indices.shape[3],
+                            counts.data_ptr(), i64_array(counts.stride()), float(sm_scale), int(block_size),
+                            out.data_ptr(), lse.data_ptr() if lse is not None else None,
+                            ws.data_ptr() if ws is not None else None, ws_bytes,
+                            _lib.LI_BSA_BALANCE if balance else 0, _stream(dev))
+    if st == _lib.LI_ERR_K_LEN:
+        raise ValueError(f"K Length ({Lk}) must be divisible by logical_block_size ({block_size})")
+    check("li_bsa_fwd_fp8", st)
     return (out, lse) if return_lse else out

@@ -78,6 +78,11 @@ def ragged(sparse_params):
     return sparse_params.get("row_budget") is not None
 
 
+def qk_fp8(sparse_params):
+    """The ``qk_fp8`` extension key: Q K^T on e4m3 codes with per-tile-block scales."""
+    return bool(sparse_params.get("qk_fp8", False))
+
+
 def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance):
     """Pools, block selection, then one kernel that gathers, attends and untiles."""
     B, NH, _, D = q.shape
@@ -108,8 +113,58 @@ def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events
     return o_out if o_out.dtype == out_dtype else o_out.to(out_dtype)
 
 
+def fp8_supported(D, tile):
+    """Shapes the e4m3 (qk_fp8) path is built for: D = 128 and 128-token tiles."""
+    return D == 128 and tile[0] * tile[1] * tile[2] == 128
+
+
+def _tiled_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance):
+    """Tiled sequence with Q and K quantized to e4m3 per tile block (scale amax / 448) in their gathers.
+
+    The pools (and so the block selection) are those of the bf16 path; V, P V and the output stay bf16.
+    """
+    B, NH, _, D = q.shape
+    dev = q.device
+    f8 = _core.FP8
+    _stage(events, "alloc_start")
+    q8 = torch.empty((B, NH, g.nq_blk, g.bs, D), device=dev, dtype=f8)
+    q_scale = torch.empty((B, NH, g.nq_blk), device=dev, dtype=torch.float32)
+    q_pool = torch.empty((B, NH, g.nq_blk, D), device=dev, dtype=q.dtype)
+    nkb = g.num_txt_blk + g.nk_blk
+    k8 = torch.empty((B, NH, nkb, g.bs, D), device=dev, dtype=f8)
+    k_scale = torch.empty((B, NH, nkb), device=dev, dtype=torch.float32)
+    v_all = torch.empty((B, NH, nkb, g.bs, D), device=dev, dtype=q.dtype)
+    k_pool = torch.empty((B, NH, g.nk_blk, D), device=dev, dtype=q.dtype)
+    if text_len > 0:
+        pad = g.num_txt_blk * g.bs - text_len
+        kt = F.pad(k_txt, (0, 0, 0, pad)) if pad > 0 else k_txt
+        vt = F.pad(v_txt, (0, 0, 0, pad)) if pad > 0 else v_txt
+        v_all[:, :, :g.num_txt_blk].copy_(vt.reshape(B, NH, g.num_txt_blk, g.bs, D))
+    _stage(events, "alloc_end")
+    _stage(events, "prep_start")
+    if text_len > 0:
+        # Contiguous text blocks: the trivial grid T = blocks, H = 1, W = BS, tile (1, 1, BS).
+        _core.tile_prep_fp8(kt, k8, k_scale, None, 0, 0, g.num_txt_blk, 1, g.bs, 1, 1, g.bs, 1, 1)
+    _core.tile_prep_fp8(q, q8, q_scale, q_pool, 0, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    _core.kv_prep_fp8(k_vis, v_vis, k8, k_scale, v_all, k_pool, g.num_txt_blk, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw,
+                      g.nh, g.nw)
+    _stage(events, "prep_end")
+    _stage(events, "index_start")
+    indices, counts = select(q_pool, k_pool, text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
+    _stage(events, "index_end")
+    _stage(events, "attn_start")
+    o_flat = _core.bsa_forward_fp8(q8.flatten(2, 3), q_scale, k8.flatten(2, 3), k_scale, v_all.flatten(2, 3),
+                                   indices, counts, 1.0 / math.sqrt(D), g.bs, balance=balance)
+    _stage(events, "attn_end")
+    _stage(events, "untile_start")
+    o_out = torch.empty_like(q)
+    _core.untile(o_flat.view(B, NH, g.nq_blk, g.bs, D), o_out, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    _stage(events, "untile_end")
+    return o_out if o_out.dtype == out_dtype else o_out.to(out_dtype)
+
+
 def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, events=None, fused=True,
-                     balance=False):
+                     balance=False, qk_fp8=False):
     """One sparse-attention forward.
 
     q (B,H,Lq,D); k_txt/v_txt (B,H,N_txt,D) or None; k_vis/v_vis (B,H,Lk,D), any strides.
@@ -120,7 +175,8 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
     at least one tile high and wide, token views with unit d stride);
     otherwise, or with ``fused=False``, the tiled sequence q_prep / kv_prep /
     attention / untile.  Both give the same bits.  ``balance`` (rows with their own budgets) starts
-    the longest query tiles first.
+    the longest query tiles first.  ``qk_fp8`` takes Q K^T on e4m3 codes with one scale per tile
+    block (bf16 only; D = 128 and 128-token tiles, ValueError otherwise); the selection is unchanged.
     """
     out_dtype = q.dtype
     if q.dtype not in (torch.bfloat16, torch.float16):
@@ -131,6 +187,11 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
     g = geometry(latent_hw, tile, q.shape[2], k_vis.shape[2], text_len)
     B, NH, _, D = q.shape
     dev, dt = q.device, q.dtype
+    if qk_fp8:
+        if dt != torch.bfloat16 or not fp8_supported(D, tile):
+            raise ValueError(f"qk_fp8 is built for bfloat16, D = 128 and 128-token tiles (got {dt}, D = {D}, "
+                             f"tile {tuple(tile)})")
+        return _tiled_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance)
     if fused and uses_fused(q, k_vis, v_vis, tile, (g.H, g.W)):
         return _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance)
     _stage(events, "alloc_start")

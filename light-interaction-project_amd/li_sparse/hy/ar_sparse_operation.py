@@ -8,8 +8,10 @@ with every kernel a gfx950 HIP kernel of this package.
 ``sparse_params`` keys: ``tile_size`` (default (4, 8, 4)), ``topk_ratio``,
 ``recent_protect``, ``sim_metric`` as in the reference; optional extensions
 ``force_diag`` / ``force_sink`` (keep the query's own key block and the
-t-slab-0 block at its (h, w)) and ``row_budget`` (explicit per-row totals).
-Unset, they leave the reference's selection unchanged.
+t-slab-0 block at its (h, w)), ``row_budget`` (explicit per-row totals) and
+``qk_fp8`` (Q K^T on e4m3 codes with one fp32 scale per tile block; the
+selection is unchanged).  Unset, they leave the reference's behaviour
+unchanged.
 """
 import torch
 import torch.nn.functional as F
@@ -69,4 +71,5 @@ def run_sparse_attention(q, k_txt, v_txt, k_vis, v_vis, block_idx, latent_hw, sp
                                      q.device)
 
     return _pipeline.sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select,
-                                      balance=_pipeline.ragged(sparse_params))
+                                      balance=_pipeline.ragged(sparse_params),
+                                      qk_fp8=_pipeline.qk_fp8(sparse_params))

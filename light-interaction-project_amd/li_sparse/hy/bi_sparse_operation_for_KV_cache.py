@@ -4,7 +4,9 @@ Mirrors hy-worldplay/files/hyvideo/models/transformers/modules/bi_sparse_operati
 ``generate_prefill_indices`` (:220-296) and ``run_sparse_prefill_attention``
 (:301-395): dense SDPA for the first three chunks or untileable shapes
 (:329-343), otherwise the sparse pipeline with the 3D-neighbour forced set
-and the ``min(max(int(Nk*ratio), 7), Nk)`` budget.
+and the ``min(max(int(Nk*ratio), 7), Nk)`` budget.  The extension keys of
+ar_sparse_operation (``force_diag``, ``force_sink``, ``row_budget``,
+``qk_fp8``) apply here too.
 """
 import torch
 import torch.nn.functional as F
@@ -54,4 +56,5 @@ def run_sparse_prefill_attention(q, k_txt, v_txt, k_vis, v_vis, block_idx, laten
                                         q.device)
 
     return _pipeline.sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select,
-                                      balance=_pipeline.ragged(sparse_params))
+                                      balance=_pipeline.ragged(sparse_params),
+                                      qk_fp8=_pipeline.qk_fp8(sparse_params))

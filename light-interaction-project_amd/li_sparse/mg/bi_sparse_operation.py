@@ -5,7 +5,9 @@ Mirrors matrix-game-3.0/files/wan/modules/bi_sparse_operation.py:
 ``generate_prefill_indices`` (:179-234, default ratio 0.25) and
 ``run_sparse_attention(q, k, v, text_len, ...)`` (:236-348) on a combined
 text+visual K/V, tile default (4, 4, 8), with the optional per-stage event
-timing of the reference (``ENABLE_SPARSE_PROFILING``, :13, 237-346).
+timing of the reference (``ENABLE_SPARSE_PROFILING``, :13, 237-346).  The
+extension keys of the HY module (``force_diag``, ``force_sink``,
+``row_budget``, ``qk_fp8``) apply here too.
 """
 import torch.nn.functional as F
 
@@ -40,7 +42,8 @@ def run_sparse_attention(q, k, v, text_len, block_idx, latent_hw, sparse_params)
         return generate_prefill_indices(q_pool, k_pool, tl, grid_k, dict(sparse_params, tile_size=tile), q.device)
 
     o = _pipeline.sparse_attention(q, k_txt, v_txt, k[:, :, text_len:], v[:, :, text_len:], latent_hw, tile,
-                                   select, events, balance=_pipeline.ragged(sparse_params))
+                                   select, events, balance=_pipeline.ragged(sparse_params),
+                                   qk_fp8=_pipeline.qk_fp8(sparse_params))
     if events is not None:
         torch.cuda.synchronize()
         t = lambda a, b: events[a].elapsed_time(events[b])  # noqa: E731

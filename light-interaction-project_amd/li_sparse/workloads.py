@@ -31,6 +31,7 @@ class Workload:
     force_diag: bool = True
     force_sink: bool = True
     ragged: tuple = None          # (min, max) per-row totals when rows are ragged
+    qk_fp8: bool = False          # Q K^T on e4m3 codes with per-tile-block scales
     note: str = ""
 
     @property
@@ -46,6 +47,8 @@ class Workload:
              "force_diag": self.force_diag, "force_sink": self.force_sink}
         if self.ragged is not None:
             p["row_budget"] = ragged_budgets(nq_blk, *self.ragged)
+        if self.qk_fp8:
+            p["qk_fp8"] = True
         return p
 
 
@@ -67,6 +70,9 @@ WORKLOADS = {
                         "2x8x8 tiles, 25% keep + diag + sink"),
     "hy_long": Workload("hy_long", 16, 128, (30, 52), 4, 64, (2, 8, 8), 0.1, "scaled_dot_product", ragged=(8, 200),
                         note="HY long rollout: Lq=6240, Lk=99840 (64 frames), ragged rows 8..200 blocks (~10%)"),
+    "hy_fp8": Workload("hy_fp8", 16, 128, (30, 52), 4, 12, (2, 8, 8), 0.3, "scaled_dot_product", qk_fp8=True,
+                       note="HY shape with Q, K as e4m3 codes and per-128-token-block fp32 scales (amax/448), "
+                            "V bf16: e4m3 MFMA for Q K^T, bf16 for P V; the same selection as hy"),
 }
 
 

@@ -5,6 +5,7 @@ import numpy as np
 import torch
 
 from oracle import attention as oatt
+from oracle import fp8 as ofp8
 from oracle import mask as omask
 from oracle import tile as otile
 from oracle.bf16 import bf16_to_f32
@@ -38,7 +39,8 @@ def oracle_pipeline(q, k, v, latent_hw, params, mode="decode", text=None, heads=
     """Oracle of run_sparse_attention on CPU tensors.
 
     Returns dict with tiles/pools (bits), indices/counts, scores, tie_free, out (float64, linear layout).
-    ``heads`` restricts the attention to a list of (b, h, m) tiles.
+    ``heads`` restricts the attention to a list of (b, h, m) tiles.  With ``params["qk_fp8"]`` the
+    attention takes Q and K (text blocks included) as their per-block e4m3 quantizations, dequantized.
     """
     H, W = latent_hw
     tile = tuple(params["tile_size"])
@@ -62,6 +64,9 @@ def oracle_pipeline(q, k, v, latent_hw, params, mode="decode", text=None, heads=
         vtx = np.concatenate([bf16_to_f32(bits(text[1])), np.zeros((B, NH, pad, D), np.float32)], axis=2)
         kf, vf = np.concatenate([ktx, kf], axis=2), np.concatenate([vtx, vf], axis=2)
     qf = bf16_to_f32(qt.reshape(B, NH, -1, D))
+    if params.get("qk_fp8", False):
+        qf = ofp8.dequantize_blocks(*ofp8.quantize_blocks(qf.reshape(B, NH, -1, bs, D))).reshape(B, NH, -1, D)
+        kf = ofp8.dequantize_blocks(*ofp8.quantize_blocks(kf.reshape(B, NH, -1, bs, D))).reshape(B, NH, -1, D)
     o, lse = oatt.bsa_forward(qf, kf, vf, ind, cnt, 1.0 / math.sqrt(D), bs, heads=heads)
     perm = tile_permutation(geo["T_q"], H, W, tile)
     valid = perm >= 0
