@@ -79,14 +79,19 @@ def mean(xs):
     return sum(xs) / len(xs)
 
 
-def load_traffic(kernel):
-    """HBM bytes per launch of ``kernel`` from the committed counter summary, or None.
+TRAFFIC_SUMMARIES = {"hy": "bsa_fwd_hy_traffic.md", "hy_fp8": "bsa_fwd_e4m3_hy_traffic.md"}
 
-    The summary (profiles/bsa_fwd_hy_traffic.md) holds rocprofv3 FETCH_SIZE and
+
+def load_traffic(kernel, workload):
+    """HBM bytes per launch of ``kernel`` from the committed counter summary of ``workload``, or None.
+
+    The summaries (profiles/bsa_fwd_*hy_traffic.md) hold rocprofv3 FETCH_SIZE and
     WRITE_SIZE per dispatch, each scaled by the factor the same counter reads
     for a copy kernel of known size in the same run.
     """
-    path = os.path.join(REPO, "profiles", "bsa_fwd_hy_traffic.md")
+    if workload not in TRAFFIC_SUMMARIES:
+        return None
+    path = os.path.join(REPO, "profiles", TRAFFIC_SUMMARIES[workload])
     try:
         with open(path) as f:
             for line in f:
@@ -169,7 +174,8 @@ def main():
         attn = lambda: _core.bsa_forward_fp8(q8f, qs, k8f, ks, vf, ind, cnt, scale, bs, balance=balance)  # noqa
 
     if args.profile:
-        profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params, ind, cnt, flops, dev)
+        profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params, ind, cnt, flops, dev,
+                        fp8_tiles=(q8, qs, k8, ks) if fp8 else None)
         return
 
     for _ in range(5):
@@ -259,7 +265,7 @@ def main():
                      "frac": round(attn_tflops / peak, 4),
                      "peak_note": ("half the FLOPs (Q K^T) at the 5.0 PFLOP/s fp8 peak, half (P V) at the "
                                    "2.5 PFLOP/s bf16 peak") if fp8 else "dense bf16 MFMA peak",
-                     "traffic": load_traffic(kname) if args.workload == "hy" else None,
+                     "traffic": load_traffic(kname, args.workload),
                      "traffic_unit": "bytes per launch (HBM/MALL side, rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
         "fused_path": fused,
         "prep_bytes_per_call": prep_bytes,
@@ -270,7 +276,8 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params, ind, cnt, flops, dev):
+def profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params, ind, cnt, flops, dev,
+                    fp8_tiles=None):
     """Each kernel of one call, --steps launches apiece, for rocprofv3 kernel traces and counters."""
     import torch
 
@@ -285,12 +292,25 @@ def profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params
     o_tok = torch.empty_like(qd)
     src = torch.empty(1 << 27, dtype=torch.bfloat16, device=dev).fill_(1.0)   # 256 MiB
     dst = torch.empty_like(src)
-    fused = _pipeline.uses_fused(qd, kd, vd, wl.tile, wl.latent_hw)
+    fp8 = fp8_tiles is not None
+    fused = _pipeline.uses_fused(qd, kd, vd, wl.tile, wl.latent_hw) and not fp8
     balance = _pipeline.ragged(params)
     q_pool = torch.empty_like(q_p)
     k_pool = torch.empty_like(k_p)
     for _ in range(args.steps):
-        if fused:
+        if fp8:
+            # The e4m3 call's kernels: quantizing Q gather + pool, quantizing K
+            # gather + V gather + K pool, block mask, e4m3 attention (+ merge),
+            # untile; then the bf16 tiled attention on the same lists.
+            q8, qs, k8, ks = fp8_tiles
+            _core.tile_prep_fp8(qd, q8, qs, q_pool, 0, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+            _core.kv_prep_fp8(kd, vd, k8, ks, v_all, k_pool, 0, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+            fast_generate_indices(q_pool, k_pool, 0, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), params, dev)
+            _core.bsa_forward_fp8(q8.flatten(2, 3), qs, k8.flatten(2, 3), ks, vf, ind, cnt, scale, bs, out=out,
+                                  balance=balance)
+            _core.untile(out.view(B, H, g.nq_blk, bs, D), o_lin, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+            _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs, out=out, balance=balance)
+        elif fused:
             # The call's own kernels: Q pool, K pool, block mask, fused
             # attention (+ its tail merge); then the tiled attention kernel on
             # the same lists, for comparison.
@@ -316,7 +336,13 @@ def profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params
                                    "written once for the fused kernel (Q + K + V tiles read once for the tiled one)"},
         "copy (calibration)": {"bytes_read": src.numel() * e, "bytes_written": dst.numel() * e},
     }
-    if fused:
+    if fp8:
+        alg["bsa_fwd_kernel"]["bytes_min_e4m3"] = (1 * (g.nq_blk + g.nk_blk) + 2 * g.nk_blk + 2 * g.nq_blk) * bs * H * D * B
+        alg["gather_fp8_kernel<1> (Q)"] = {"bytes": H * D * B * (e * wl.lq + g.nq_blk * bs) + e * H * D * g.nq_blk}
+        alg["gather_fp8_kernel<2> (K e4m3, V)"] = {"bytes": H * D * B * (2 * e * wl.lk + (1 + e) * g.nk_blk * bs)
+                                                   + e * H * D * g.nk_blk}
+        alg["untile_kernel"] = {"bytes": e * H * D * B * 2 * wl.lq}
+    elif fused:
         alg["bsa_fwd_kernel"]["bytes_min_fused"] = e * (2 * wl.lq + 2 * wl.lk) * H * D * B
         alg["pool (Q)"] = {"bytes": e * H * D * B * wl.lq + e * H * D * g.nq_blk, "grid_blocks": g.nq_blk}
         alg["pool (K)"] = {"bytes": e * H * D * B * wl.lk + e * H * D * g.nk_blk, "grid_blocks": g.nk_blk}
@@ -325,7 +351,7 @@ def profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params
         alg["gather_pool_kernel<2> (K,V)"] = {"bytes": e * H * D * B * 2 * (wl.lk + g.nk_blk * bs)
                                               + e * H * D * g.nk_blk}
         alg["untile_kernel"] = {"bytes": e * H * D * B * 2 * wl.lq}
-    print(json.dumps({"profile": wl.name, "fused": fused, "launches_per_kernel": args.steps,
+    print(json.dumps({"profile": wl.name, "fused": fused, "e4m3": fp8, "launches_per_kernel": args.steps,
                       "algorithmic_per_launch": alg}), flush=True)
 
 

@@ -26,7 +26,7 @@ from oracle.geometry import block_geometry
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-2          # bf16 output vs the float64 oracle on the same (dequantized) Q/K
-FP8_VS_BF16 = 6e-2  # bf16 output of the e4m3 call vs the bf16 call, max abs, HY-shaped inputs
+FP8_VS_BF16 = 1e-2  # e4m3 call vs bf16 call, max abs, HY shape (measured 3.9e-3; mean abs 6.9e-5)
 
 
 def _codes(t):
