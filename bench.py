@@ -203,6 +203,16 @@ def main():
              "torch_sdpa_tflops": round(dense_flops / (dense_ms * 1e-3) / 1e12, 2),
              "speedup_call_vs_sdpa": round(dense_ms / step_ms, 3),
              "speedup_attention_vs_sdpa": round(dense_ms / attn_ms, 3)}
+    if _core.dense_supported(qd, kd, vd):
+        # This library's dense kernel (li_attn_fwd_dense) on the same valid tokens.
+        own = lambda: _core.attn_dense(qd, kd, vd)  # noqa: E731
+        own()
+        _, own_per = event_loop(own, max(5, args.steps // 5), stream)
+        own_ms = mean(own_per)
+        dense.update({"own_dense_kernel_ms": round(own_ms, 4),
+                      "own_dense_kernel_tflops": round(dense_flops / (own_ms * 1e-3) / 1e12, 2),
+                      "speedup_call_vs_own_dense": round(own_ms / step_ms, 3),
+                      "speedup_attention_vs_own_dense": round(own_ms / attn_ms, 3)})
     if args.compare_dense:
         all_ind = torch.arange(g.nk_blk, dtype=torch.int32, device=dev).expand(B, H, g.nq_blk, g.nk_blk).contiguous()
         all_cnt = torch.full((B, H, g.nq_blk), g.nk_blk, dtype=torch.int32, device=dev)

@@ -230,6 +230,31 @@ int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D,
 int64_t li_bsa_fwd_workspace_size(int32_t B, int32_t NH, int32_t Lq, int32_t D, int32_t block_size);
 
 /*
+ * Dense attention over all keys: the reference's dense fallback
+ * F.scaled_dot_product_attention(q, cat(k_txt, k_vis), cat(v_txt, v_vis))
+ * (HYAR:316-317; HYKV:331-343; MGS:246-248), with the concatenation never
+ * formed.  out = softmax(sm_scale q K^T) V over the txt_len text keys and the
+ * Lk visual keys, no padding key taking part; P is rounded to the element
+ * type before P V, as on the sparse path.
+ *   q (B, NH, Lq, D), k / v (B, NH, Lk, D), out (B, NH, Lq, D): token views,
+ *     any batch/head/token strides (multiples of 8 elements, unit d stride,
+ *     16-byte aligned), K/V token strides >= D.
+ *   k_txt / v_txt: (B, NH, ceil(txt_len/128)*128, D) contiguous text keys/values
+ *     (rows past txt_len are ignored), or NULL when txt_len = 0.
+ *   lse: (B, NH, ceil(Lq/128)*128) fp32 (log2 units; rows past Lq belong to zero
+ *     queries), or NULL.  workspace as for li_bsa_fwd (size function with
+ *     Lq = ceil(Lq/128)*128).
+ * Built for D = 128 and Lk a multiple of 4 (LI_ERR_UNSUPPORTED otherwise).
+ */
+int li_attn_fwd_dense(int dtype, int32_t B, int32_t NH, int32_t D, int32_t Lq, int32_t Lk,
+                      const void* q, const int64_t q_strides[4],
+                      const void* k, const int64_t k_strides[4],
+                      const void* v, const int64_t v_strides[4],
+                      const void* k_txt, const void* v_txt, int32_t txt_len,
+                      float sm_scale, void* out, const int64_t out_strides[4], float* lse,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * fp8 variant of the tiled path: Q and K as OCP e4m3 (float8_e4m3fn) codes
  * with one fp32 scale per tile block, V bf16.  The reference has no fp8
  * path; these mirror li_q_prep / li_kv_prep / li_bsa_fwd (HYAR:166-202,

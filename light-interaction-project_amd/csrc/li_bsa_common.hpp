@@ -26,6 +26,14 @@ struct BsaGather {
   uint32_t mg_nhnw, mg_nw, mg_thtw, mg_tw;
   // ~0 where the matching divisor is 1, else 0 (the identity term of udiv16m).
   uint32_t id_nhnw, id_nw;
+  // Token bounds: query rows at tokens >= q_tokens are neither read nor
+  // stored, and visual K/V chunks starting at tokens >= k_tokens are read as
+  // zeros (Tq*H*W and Tk*H*W on the sparse path, where the grid bounds
+  // decide).  Dense calls: the last text block keeps txt_tail rows and the
+  // last visual block vis_tail rows, the others get score -inf (0 = all
+  // rows kept, zero rows included, as on the sparse path).
+  int32_t q_tokens, k_tokens;
+  int32_t txt_tail, vis_tail;
 };
 
 // Kernel arguments of the attention forward (all pointers are device
@@ -34,6 +42,8 @@ struct BsaArgs {
   const uint16_t* q;
   const uint16_t* k;
   const uint16_t* v;
+  // Kept block ids (B, NH, nqt, n_cols) and their counts (B, NH, nqt), or
+  // null for every tile keeping blocks 0 .. n_cols - 1 in order (dense calls).
   const int32_t* idx;
   int64_t is[4];
   const int32_t* cnt;

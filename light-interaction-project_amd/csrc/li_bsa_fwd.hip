@@ -427,11 +427,15 @@ __device__ __forceinline__ void sched_m_phase() {
 // 16-bit.  The e4m3 K stage has 128-byte rows with no padding: the 16-byte
 // granule g of row r sits at slot g ^ ((r >> 1) & 7), so the 16 rows a
 // 16-lane group reads (any 16 aligned rows) fall in 16 distinct bank windows.
-template <typename E, int BS, bool G = false, bool F8 = false>
+// DN (dense calls, token-order addressing only): no index lists, every tile
+// keeps blocks 0 .. n_cols - 1; queries and keys past the token bounds are
+// skipped, and the padding rows of the last text and visual blocks score -inf.
+template <typename E, int BS, bool G = false, bool F8 = false, bool DN = false>
 __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   using C = DmaCfg<BS>;
   static_assert(!G || BS == 128, "token-order addressing is built for 128-row tiles");
   static_assert(!F8 || (BS == 128 && !G), "the e4m3 kernel is built for tiled 128-row blocks");
+  static_assert(!DN || G, "dense calls use token-order addressing");
   constexpr int D = 128;
   typedef typename E::vec8 vec8;
   typedef __attribute__((address_space(3))) void lds_void;
@@ -471,13 +475,16 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   uint16_t* ohead = a.out + (int64_t)bh * a.Lq * D;
   constexpr int KEB = F8 ? 1 : 2;  // bytes per K element
   const char* kbytes = reinterpret_cast<const char*>(a.k) + (int64_t)bh * a.nkb * BS * D * KEB;
-  const int32_t* irow = a.idx + b * a.is[0] + h * a.is[1] + (int64_t)m * a.is[2];
-  int count = a.cnt[b * a.cs[0] + h * a.cs[1] + (int64_t)m * a.cs[2]];
+  // Dense calls: tile m keeps blocks 0 .. n_cols - 1, ids id_base + i.
+  const int32_t* irow = DN ? nullptr : a.idx + b * a.is[0] + h * a.is[1] + (int64_t)m * a.is[2];
+  int count = DN ? a.n_cols : a.cnt[b * a.cs[0] + h * a.cs[1] + (int64_t)m * a.cs[2]];
   count = count < 0 ? 0 : (count > a.n_cols ? a.n_cols : count);
   count = __builtin_amdgcn_readfirstlane(count);
+  int id_base = 0;
   if (half >= 0) {
     const int h0 = (count + 1) >> 1;
-    irow += half ? (int64_t)h0 * a.is[3] : 0;
+    if constexpr (!DN) irow += half ? (int64_t)h0 * a.is[3] : 0;
+    id_base = half ? h0 : 0;
     count = half ? count - h0 : h0;
   }
   const int row0 = m * BS;
@@ -491,7 +498,8 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     if constexpr (G) {
       bool ok;
       const int32_t l = tile_token(a.g, a.g.Tq, m, rt, ok);
-      return ok ? a.out + b * a.g.os[0] + h * a.g.os[1] + (int64_t)l * a.g.os[2] : nullptr;
+      return ok && (!DN || l < a.g.q_tokens) ? a.out + b * a.g.os[0] + h * a.g.os[1] + (int64_t)l * a.g.os[2]
+                                             : nullptr;
     } else {
       return row0 + rt < a.Lq ? ohead + (int64_t)(row0 + rt) * D : nullptr;
     }
@@ -540,7 +548,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     if constexpr (G) {
       bool ok;
       const int32_t l = tile_token(a.g, a.g.Tq, m, 32 * qq + l32, ok);
-      if (ok) qrow = a.q + b * a.g.qs[0] + h * a.g.qs[1] + (int64_t)l * a.g.qs[2];
+      if (ok && (!DN || l < a.g.q_tokens)) qrow = a.q + b * a.g.qs[0] + h * a.g.qs[1] + (int64_t)l * a.g.qs[2];
     } else {
       const int r = row0 + 32 * qq + l32;
       if (r < a.Lq) qrow = qhead + (int64_t)r * D;
@@ -643,14 +651,14 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   // the block max is not computed at all on the common path; the result is
   // the same softmax.
   u32x4 ppk[C::PST];
-  auto exps = [&]() LI_INLINE {
+  auto exps = [&](float off) LI_INLINE {
     float ls = 0.0f;
 #pragma unroll
     for (int st = 0; st < C::PST; ++st) {
       const int kt = st >> 1, ip = st & 1;
       float pv[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][8 * ip + e], qk_scale, -mrow));
+      for (int e = 0; e < 8; ++e) pv[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[kt][8 * ip + e], qk_scale, -off));
       float s2 = (pv[0] + pv[1]) + (pv[2] + pv[3]);
       float s3 = (pv[4] + pv[5]) + (pv[6] + pv[7]);
       ls += s2 + s3;
@@ -659,8 +667,11 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     }
     return ls;
   };
+  // A lane whose keys so far all scored -inf (keys masked on dense calls)
+  // keeps mrow = -inf, l = 0 and O = 0: the slow path then takes its
+  // exponentials against 0 instead (all zero), never against -inf.
   auto softmax = [&]() LI_INLINE {
-    float ls = exps();
+    float ls = exps(mrow);
     if (__ballot(!(ls <= 1048576.0f))) {
       float mx = sacc[0][0];
 #pragma unroll
@@ -670,14 +681,15 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
       mx = __builtin_fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * qk_scale;
       const float mnew = __builtin_fmaxf(mrow, mx);
-      const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);
+      const float msafe = mnew == -__builtin_inff() ? 0.0f : mnew;
+      const float alpha = __builtin_amdgcn_exp2f(mrow - msafe);
       mrow = mnew;
       lrow *= alpha;
 #pragma unroll
       for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-      ls = exps();
+      ls = exps(msafe);
     }
     lrow += ls;
   };
@@ -700,7 +712,13 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   // Block ids are wave-uniform: read them through the scalar cache.
   typedef __attribute__((address_space(4))) const int32_t const_i32;
   const_i32* irow_s = (const_i32*)irow;
-  auto block_id = [&](int i) LI_INLINE { return irow_s[(int64_t)(i < count ? i : count - 1) * a.is[3]]; };
+  auto block_id = [&](int i) LI_INLINE {
+    const int j = i < count ? i : count - 1;
+    if constexpr (DN)
+      return id_base + j;
+    else
+      return (int)irow_s[(int64_t)j * a.is[3]];
+  };
   auto valid = [&](int id_) LI_INLINE { return (unsigned)id_ < (unsigned)a.nkb; };
   auto safe = [&](int id_) LI_INLINE { return valid(id_) ? id_ : 0; };
 
@@ -776,6 +794,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
 
     uint32_t kvo[LPW], vvo[LPW];
     uint32_t lane_ft = 0, lane_fh = 0, lane_fw = 0;
+    int32_t lane_coff = 0;  // token offset of chunk lane % 32 from its block's first token
     const char* vis_k = nullptr;
     const char* vis_v = nullptr;
     const char* txt_k = nullptr;
@@ -802,6 +821,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
         vvo[j] = coff * (uint32_t)(2 * a.g.vs[2]) + v_src_vis - (j & 3) * 1024;
       }
       coords(lane & 31, lane_ft, lane_fh, lane_fw);
+      if constexpr (DN) lane_coff = (int32_t)((lane_ft * a.g.H + lane_fh) * a.g.W + lane_fw);
     }
     // A key block's geometry, shared by its K and V loads: its first token
     // and this wave's in-grid chunk mask (0 for text blocks).  A block is a
@@ -828,7 +848,8 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
         const uint32_t ch = udiv16m(rem, a.g.mg_nw, a.g.id_nw), cw = rem - ch * (uint32_t)a.g.nw;
         const uint32_t t0 = ct * a.g.tt, h0 = ch * a.g.th, w0 = cw * a.g.tw;
         g_.l0 = (int32_t)((t0 * a.g.H + h0) * a.g.W + w0);
-        const bool inside = (lane_ft < a.g.Tk - t0) & (lane_fh < a.g.H - h0) & (lane_fw < a.g.W - w0);
+        const bool inside = (lane_ft < a.g.Tk - t0) & (lane_fh < a.g.H - h0) & (lane_fw < a.g.W - w0) &
+                            (!DN || (int32_t)g_.l0 + lane_coff < a.g.k_tokens);
         const uint32_t in_grid = (uint32_t)__ballot(inside);
         g_.mask = (in_grid >> (gw * LPW)) & (txt ? 0u : (1u << LPW) - 1u);
         g_.txt = txt;
@@ -941,11 +962,29 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       }
       sched_m_phase<NPV, F8 ? 2 : 1, NU, LA>();
     };
+    // Dense calls: the keys past the end of the last text block and of the
+    // last visual block get score -inf.  Element r of sacc[kt] holds key
+    // KW*kh + 32*kt + kperm(8*(r/4) + 4*hl + r%4) of the block.
+    auto mask_tail = [&](int blk) LI_INLINE {
+      if constexpr (DN) {
+        int nv = BS;
+        if (a.g.txt_tail > 0 && blk == a.g.ntxt - 1) nv = a.g.txt_tail;
+        if (a.g.vis_tail > 0 && blk == a.nkb - 1) nv = a.g.vis_tail;
+        if (nv < BS) {
+#pragma unroll
+          for (int kt = 0; kt < C::NKT; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              if (C::KW * kh + 32 * kt + kperm(8 * (r >> 2) + 4 * hl + (r & 3)) >= nv) sacc[kt][r] = -__builtin_inff();
+        }
+      }
+    };
     // pre() runs at the head of either branch, where its scalar work can
     // interleave with the softmax's vector work.
     auto x_phase = [&](int blk, auto&& pre) LI_INLINE {
       if (valid(blk)) {
         pre();
+        mask_tail(blk);
         softmax();
       } else {
         pre();
@@ -959,7 +998,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     // The next id to read, stepped along the row and held at its last entry
     // (the same clamp as block_id), so a read costs no index arithmetic.
     const int64_t ist = a.is[3];
-    const_i32* idp = irow_s + (int64_t)(count > 4 ? 4 : (count > 0 ? count - 1 : 0)) * ist;
+    const_i32* idp = DN ? nullptr : irow_s + (int64_t)(count > 4 ? 4 : (count > 0 ? count - 1 : 0)) * ist;
     Blk dv{nullptr, nullptr, 0u}, dk{nullptr, nullptr, 0u};
     Geo geo_k{0, 0, 0u, false};  // geometry of the K block of the next M phase
     // F8: K scales of blocks id_n and id_nn, read one pair ahead of their
@@ -1000,8 +1039,12 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       id_c = id_n;
       id_n = id_nn;
       id_nn = id_n3;
-      id_n3 = *idp;
-      idp = i + 5 < count ? idp + ist : idp;
+      if constexpr (DN) {
+        id_n3 = id_base + (i + 4 < count ? i + 4 : count - 1);
+      } else {
+        id_n3 = *idp;
+        idp = i + 5 < count ? idp + ist : idp;
+      }
       if constexpr (F8) {
         qk_scale = qk_base * sk_n;
         sk_n = sk_nn;
@@ -1152,7 +1195,7 @@ __global__ __launch_bounds__(256) void bsa_merge_kernel(BsaArgs a) {
     const int b = bh / a.NH, h = bh % a.NH;
     bool ok;
     const int32_t l = tile_token(a.g, a.g.Tq, m, rt, ok);
-    if (ok) orow = a.out + b * a.g.os[0] + h * a.g.os[1] + (int64_t)l * a.g.os[2] + 16 * dq;
+    if (ok && l < a.g.q_tokens) orow = a.out + b * a.g.os[0] + h * a.g.os[1] + (int64_t)l * a.g.os[2] + 16 * dq;
   } else {
     orow = a.out + ((int64_t)bh * a.Lq + r) * D + 16 * dq;
   }
@@ -1188,12 +1231,12 @@ __global__ __launch_bounds__(256) void bsa_merge_kernel(BsaArgs a) {
   if (a.lse && dq == 0) a.lse[(int64_t)bh * a.Lq + r] = none ? -__builtin_inff() : mm + __builtin_log2f(l);
 }
 
-template <typename E>
+template <typename E, bool DN = false>
 int launch_bsa_gather(BsaArgs& a, int tiles, hipStream_t s) {
   const int nsplit = tiles - a.n_full;
   clear_launch_error();
-  hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, 128, true>), dim3(a.n_full + 2 * nsplit), dim3(DmaCfg<128>::NTHR), 0, s,
-                     a);
+  hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, 128, true, false, DN>), dim3(a.n_full + 2 * nsplit),
+                     dim3(DmaCfg<128>::NTHR), 0, s, a);
   if (nsplit > 0) hipLaunchKernelGGL((bsa_merge_kernel<E, true>), dim3(4 * nsplit), dim3(256), 0, s, a);
   return launch_status();
 }
@@ -1283,7 +1326,7 @@ __global__ __launch_bounds__(1024) void bsa_order_kernel(BsaArgs a, int32_t* ord
   auto bucket = [&](int tile) {
     const int bh = tile / a.nqt, m = tile % a.nqt;
     const int b = bh / a.NH, h = bh % a.NH;
-    int c = a.cnt[b * a.cs[0] + h * a.cs[1] + (int64_t)m * a.cs[2]];
+    int c = a.cnt ? a.cnt[b * a.cs[0] + h * a.cs[1] + (int64_t)m * a.cs[2]] : nc;
     c = c < 0 ? 0 : (c > nc ? nc : c);
     return nc < 1024 ? nc - c : (int)(((int64_t)(nc - c) * 1023) / nc);
   };
@@ -1504,6 +1547,10 @@ extern "C" int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D, co
   g.mg_tw = magic16(gq.tw);
   g.id_nhnw = gq.nh * gq.nw == 1 ? ~0u : 0u;
   g.id_nw = gq.nw == 1 ? ~0u : 0u;
+  g.q_tokens = gq.T * gq.H * gq.W;
+  g.k_tokens = gk.T * gk.H * gk.W;
+  g.txt_tail = 0;
+  g.vis_tail = 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int st = plan_units(a, tiles, D, 128, workspace, workspace_bytes, flags, s);
   if (st != LI_OK) return st;
@@ -1552,4 +1599,79 @@ extern "C" int li_bsa_fwd_fp8(int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int
   const int st = plan_units(a, tiles, D, block_size, workspace, workspace_bytes, flags, s);
   if (st != LI_OK) return st;
   return launch_bsa_fp8(a, (int)tiles, s);
+}
+
+extern "C" int li_attn_fwd_dense(int dtype, int32_t B, int32_t NH, int32_t D, int32_t Lq, int32_t Lk, const void* q,
+                                 const int64_t q_strides[4], const void* k, const int64_t k_strides[4], const void* v,
+                                 const int64_t v_strides[4], const void* k_txt, const void* v_txt, int32_t txt_len,
+                                 float sm_scale, void* out, const int64_t out_strides[4], float* lse,
+                                 void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!q_strides || !k_strides || !v_strides || !out_strides) return LI_ERR_INVALID_ARG;
+  if (B <= 0 || NH <= 0 || Lq < 0 || Lk < 0 || txt_len < 0) return LI_ERR_INVALID_ARG;
+  if (dtype != LI_DTYPE_BF16 && dtype != LI_DTYPE_F16) return LI_ERR_UNSUPPORTED;
+  // Keys are read in 4-token chunks of 128-token blocks: D = 128, whole chunks.
+  if (D != 128 || Lk % 4 != 0) return LI_ERR_UNSUPPORTED;
+  if (Lk + txt_len == 0) return LI_ERR_INVALID_ARG;
+  if (!row_view_ok(q, q_strides) || !row_view_ok(out, out_strides)) return LI_ERR_INVALID_ARG;
+  if (Lk > 0 && (!row_view_ok(k, k_strides) || !row_view_ok(v, v_strides))) return LI_ERR_INVALID_ARG;
+  if (Lk > 0 && (k_strides[2] < D || v_strides[2] < D)) return LI_ERR_UNSUPPORTED;
+  if (txt_len > 0 && (!k_txt || !v_txt || !aligned16(k_txt) || !aligned16(v_txt))) return LI_ERR_INVALID_ARG;
+  const int64_t nq = (Lq + 127) / 128, nvis = (Lk + 127) / 128, ntxt = (txt_len + 127) / 128;
+  if (nq >= 65536 || nvis + ntxt >= 65536) return LI_ERR_SHAPE;
+  // Byte offset of a key row from its block's first token, held in 32 bits.
+  const int64_t kv_st = Lk > 0 ? (k_strides[2] > v_strides[2] ? k_strides[2] : v_strides[2]) : 0;
+  if ((127 * kv_st + D) * 2 > (1ll << 32)) return LI_ERR_SHAPE;
+  if (Lq == 0) return LI_OK;
+  const int64_t tiles = nq * B * NH;
+  if (tiles > 0x7FFFFFFF) return LI_ERR_SHAPE;
+  BsaArgs a = {};
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.idx = nullptr;   // every tile keeps every block, in order
+  a.cnt = nullptr;
+  a.out = static_cast<uint16_t*>(out);
+  a.lse = lse;
+  a.NH = NH;
+  a.Lq = (int32_t)(nq * 128);
+  a.nkb = (int32_t)(ntxt + nvis);
+  a.nqt = (int32_t)nq;
+  a.n_cols = a.nkb;
+  a.qk_scale = sm_scale * 1.44269504f;
+  // The token sequence as a grid of 128-token rows: T = blocks, H = 1,
+  // W = 128, tile (1, 1, 128), so block t holds tokens 128 t .. 128 t + 127.
+  BsaGather& g = a.g;
+  for (int i = 0; i < 3; ++i) {
+    g.qs[i] = q_strides[i];
+    g.ks[i] = Lk > 0 ? k_strides[i] : 0;
+    g.vs[i] = Lk > 0 ? v_strides[i] : 0;
+    g.os[i] = out_strides[i];
+  }
+  g.ktxt = static_cast<const uint16_t*>(k_txt);
+  g.vtxt = static_cast<const uint16_t*>(v_txt);
+  g.ntxt = (int32_t)ntxt;
+  g.H = 1;
+  g.W = 128;
+  g.tt = 1;
+  g.th = 1;
+  g.tw = 128;
+  g.nh = 1;
+  g.nw = 1;
+  g.Tq = (int32_t)nq;
+  g.Tk = (int32_t)nvis;
+  g.mg_nhnw = magic16(1);
+  g.mg_nw = magic16(1);
+  g.mg_thtw = magic16(128);
+  g.mg_tw = magic16(128);
+  g.id_nhnw = ~0u;
+  g.id_nw = ~0u;
+  g.q_tokens = Lq;
+  g.k_tokens = Lk;
+  g.txt_tail = txt_len % 128;
+  g.vis_tail = Lk % 128;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int st = plan_units(a, tiles, D, 128, workspace, workspace_bytes, 0, s);
+  if (st != LI_OK) return st;
+  if (dtype == LI_DTYPE_BF16) return launch_bsa_gather<Bf16, true>(a, (int)tiles, s);
+  return launch_bsa_gather<F16, true>(a, (int)tiles, s);
 }

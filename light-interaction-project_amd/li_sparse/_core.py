@@ -447,3 +447,60 @@ def bsa_forward_fp8(q8, q_scale, k8, k_scale, v, indices, counts, sm_scale, bloc
         raise ValueError(f"K Length ({Lk}) must be divisible by logical_block_size ({block_size})")
     check("li_bsa_fwd_fp8", st)
     return (out, lse) if return_lse else out
+
+
+def dense_supported(q, k, v, k_txt=None):
+    """Inputs li_attn_fwd_dense takes: fp16/bf16, D = 128, Lk a multiple of 4, token views with unit d stride,
+    8-element-multiple strides, 16-byte aligned, K/V token strides >= D."""
+    if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype or q.shape[3] != 128:
+        return False
+    if k_txt is not None and k_txt.dtype != q.dtype:
+        return False
+    if k.shape[2] % 4 != 0:
+        return False
+    for t in ((q, k, v) if k.shape[2] > 0 else (q,)):
+        st = t.stride()
+        if st[3] != 1 or any(x % 8 for x in st[:3]) or st[2] < t.shape[3] or t.data_ptr() % 16:
+            return False
+    return True
+
+
+def attn_dense(q, k, v, k_txt=None, v_txt=None, sm_scale=None, return_lse=False, out=None, split=True):
+    """Dense attention over [text keys, visual keys] without forming the concatenation (see li_attn_fwd_dense).
+
+    q (B,H,Lq,128), k/v (B,H,Lk,128) token views; k_txt/v_txt (B,H,N_txt,128) or None.  Output has q's strides
+    (``empty_like(q)``).  Raises LiError(LI_ERR_UNSUPPORTED) for shapes it is not built for.
+    """
+    dev = _device_check(q, k, v)
+    _same_dtype(q, k, v)
+    B, NH, Lq, D = q.shape
+    Lk = k.shape[2]
+    if tuple(k.shape) != (B, NH, Lk, D) or tuple(v.shape) != (B, NH, Lk, D):
+        raise ValueError(f"shape mismatch q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    txt_len = 0 if k_txt is None else k_txt.shape[2]
+    kt = vt = None
+    if txt_len > 0:
+        _device_check(q, k_txt, v_txt)
+        _same_dtype(q, k_txt, v_txt)
+        if tuple(k_txt.shape) != (B, NH, txt_len, D) or tuple(v_txt.shape) != (B, NH, txt_len, D):
+            raise ValueError(f"text K/V shapes {tuple(k_txt.shape)} / {tuple(v_txt.shape)} do not match q")
+        pad = (-txt_len) % 128
+        kt = (torch.nn.functional.pad(k_txt, (0, 0, 0, pad)) if pad else k_txt).contiguous()
+        vt = (torch.nn.functional.pad(v_txt, (0, 0, 0, pad)) if pad else v_txt).contiguous()
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty_like(q)
+    nq = ceil_div(Lq, 128)
+    lse = torch.empty((B, NH, nq * 128), dtype=torch.float32, device=dev) if return_lse else None
+    with torch.cuda.device(dev):
+        ws_bytes = int(lib.li_bsa_fwd_workspace_size(B, NH, nq * 128, D, 128)) if split else 0
+    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev) if ws_bytes > 0 else None
+    st = lib.li_attn_fwd_dense(dtype_code(q), B, NH, D, Lq, Lk, q.data_ptr(), i64_array(q.stride()), k.data_ptr(),
+                               i64_array(k.stride()), v.data_ptr(), i64_array(v.stride()),
+                               kt.data_ptr() if kt is not None else None, vt.data_ptr() if vt is not None else None,
+                               txt_len, float(sm_scale), out.data_ptr(), i64_array(out.stride()),
+                               lse.data_ptr() if lse is not None else None,
+                               ws.data_ptr() if ws is not None else None, ws_bytes, _stream(dev))
+    check("li_attn_fwd_dense", st)
+    return (out, lse) if return_lse else out

@@ -226,6 +226,22 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
     return o_out if o_out.dtype == out_dtype else o_out.to(out_dtype)
 
 
+def dense_attention(q, k_txt, v_txt, k_vis, v_vis):
+    """The reference's dense fallback ``F.scaled_dot_product_attention(q, cat(k_txt, k_vis), cat(v_txt, v_vis))``
+    (ar_sparse_operation.py:316-317, bi_sparse_operation_for_KV_cache.py:331-343, bi_sparse_operation.py:246-248).
+
+    Runs the dense HIP kernel (li_attn_fwd_dense: every key, no concatenation formed) for fp16/bf16, D = 128 and
+    visual lengths that are multiples of 4; other inputs take the reference's own torch call.
+    """
+    if k_txt is not None and k_txt.shape[2] == 0:
+        k_txt = v_txt = None
+    if _core.dense_supported(q, k_vis, v_vis, k_txt):
+        return _core.attn_dense(q, k_vis, v_vis, k_txt, v_txt)
+    if k_txt is not None:
+        k_vis, v_vis = torch.cat([k_txt, k_vis], dim=2), torch.cat([v_txt, v_vis], dim=2)
+    return F.scaled_dot_product_attention(q, k_vis, v_vis, dropout_p=0.0, is_causal=False)
+
+
 def recent_blocks(params, tt, nh, nw, nk):
     """Trailing key blocks protected by ``recent_protect`` frames (ar_sparse_operation.py:263-266)."""
     rp = params.get("recent_protect", 0)

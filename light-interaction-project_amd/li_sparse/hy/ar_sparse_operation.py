@@ -13,9 +13,6 @@ t-slab-0 block at its (h, w)), ``row_budget`` (explicit per-row totals) and
 selection is unchanged).  Unset, they leave the reference's behaviour
 unchanged.
 """
-import torch
-import torch.nn.functional as F
-
 from .. import _core, _lib, _pipeline
 
 
@@ -62,8 +59,7 @@ def run_sparse_attention(q, k_txt, v_txt, k_vis, v_vis, block_idx, latent_hw, sp
     """
     LATENT_H, LATENT_W = latent_hw
     if q.shape[2] % (LATENT_H * LATENT_W) != 0:
-        return F.scaled_dot_product_attention(q, torch.cat([k_txt, k_vis], dim=2), torch.cat([v_txt, v_vis], dim=2),
-                                              is_causal=False)
+        return _pipeline.dense_attention(q, k_txt, v_txt, k_vis, v_vis)
     tile = tuple(sparse_params.get("tile_size", (4, 8, 4)))
 
     def select(q_pool, k_pool, text_len, grid_q, grid_k):

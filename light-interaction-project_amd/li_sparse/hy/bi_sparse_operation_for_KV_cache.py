@@ -8,9 +8,6 @@ and the ``min(max(int(Nk*ratio), 7), Nk)`` budget.  The extension keys of
 ar_sparse_operation (``force_diag``, ``force_sink``, ``row_budget``,
 ``qk_fp8``) apply here too.
 """
-import torch
-import torch.nn.functional as F
-
 from .. import _core, _lib, _pipeline
 from .ar_sparse_operation import launch_kv_prep, launch_q_prep, launch_untile  # noqa: F401
 from .infer_state import get_infer_state
@@ -47,8 +44,7 @@ def run_sparse_prefill_attention(q, k_txt, v_txt, k_vis, v_vis, block_idx, laten
     current_global_chunk = getattr(get_infer_state(), "current_chunk_index", 0)
     LATENT_H, LATENT_W = latent_hw
     if current_global_chunk < 3 or q.shape[2] % (LATENT_H * LATENT_W) != 0:
-        return F.scaled_dot_product_attention(q, torch.cat([k_txt, k_vis], dim=2), torch.cat([v_txt, v_vis], dim=2),
-                                              dropout_p=0.0, is_causal=False)
+        return _pipeline.dense_attention(q, k_txt, v_txt, k_vis, v_vis)
     tile = tuple(sparse_params.get("tile_size", (4, 8, 4)))
 
     def select(q_pool, k_pool, text_len, grid_q, grid_k):

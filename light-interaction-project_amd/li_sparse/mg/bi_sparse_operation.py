@@ -9,7 +9,7 @@ timing of the reference (``ENABLE_SPARSE_PROFILING``, :13, 237-346).  The
 extension keys of the HY module (``force_diag``, ``force_sink``,
 ``row_budget``, ``qk_fp8``) apply here too.
 """
-import torch.nn.functional as F
+import torch
 
 from .. import _pipeline
 from ..hy.ar_sparse_operation import launch_kv_prep, launch_q_prep, launch_untile  # noqa: F401
@@ -28,7 +28,7 @@ def run_sparse_attention(q, k, v, text_len, block_idx, latent_hw, sparse_params)
 
     LATENT_H, LATENT_W = latent_hw
     if q.shape[2] % (LATENT_H * LATENT_W) != 0:
-        return F.scaled_dot_product_attention(q, k, v, dropout_p=0.0, is_causal=False)
+        return _pipeline.dense_attention(q, None, None, k, v)
     tile = tuple(sparse_params.get("tile_size", (4, 4, 8)))
     events = {} if ENABLE_SPARSE_PROFILING else None
     if events is not None:
