@@ -153,7 +153,7 @@ def main():
     qf, kf, vf = q_t.flatten(2, 3), k_all.flatten(2, 3), v_all.flatten(2, 3)
     scale = 1.0 / math.sqrt(D)
     fp8 = bool(params.get("qk_fp8", False))
-    fused = _pipeline.uses_fused(qd, kd, vd, wl.tile, wl.latent_hw) and not fp8
+    fused = _pipeline.uses_fused(qd, kd, vd, wl.tile, wl.latent_hw)
     o_tok = torch.empty_like(qd)
     # The attention launches as the call makes them (ragged rows: longest tiles first).
     balance = _pipeline.ragged(params)
@@ -171,7 +171,12 @@ def main():
         _core.tile_prep_fp8(qd, q8, qs, None, 0, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
         _core.kv_prep_fp8(kd, vd, k8, ks, v_all, k_p, 0, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
         q8f, k8f = q8.flatten(2, 3), k8.flatten(2, 3)
-        attn = lambda: _core.bsa_forward_fp8(q8f, qs, k8f, ks, vf, ind, cnt, scale, bs, balance=balance)  # noqa
+        tiled_fp8 = lambda: _core.bsa_forward_fp8(q8f, qs, k8f, ks, vf, ind, cnt, scale, bs,  # noqa: E731
+                                                  balance=balance)
+        fused_fp8 = lambda: _core.bsa_forward_fp8_gather(  # noqa: E731
+            q8f, qs, k8f, ks, vd, None, 0, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw, ind, cnt, scale,
+            o_tok, balance=balance)
+        attn = fused_fp8 if fused else tiled_fp8
 
     if args.profile:
         profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params, ind, cnt, flops, dev,
@@ -191,6 +196,13 @@ def main():
         tiled_info = {"ms": round(tiled_ms, 4), "tflops": round(flops / (tiled_ms * 1e-3) / 1e12, 2),
                       "note": "the bf16 attention on bf16 tiles of the same inputs and lists" if fp8 else
                               "the same attention on pre-gathered tiles (the unfused sequence's kernel)"}
+    tiled_fp8_info = None
+    if fp8 and fused:
+        tiled_fp8()
+        _, t8_per = event_loop(tiled_fp8, max(5, args.steps // 5), stream)
+        t8_ms = mean(t8_per)
+        tiled_fp8_info = {"ms": round(t8_ms, 4), "tflops": round(flops / (t8_ms * 1e-3) / 1e12, 2),
+                          "note": "the e4m3 attention on V tiles (the tiled e4m3 sequence's kernel)"}
 
     # Dense comparators: torch SDPA (valid tokens) and this kernel with every block kept.
     sdpa = lambda: torch.nn.functional.scaled_dot_product_attention(qd, kd, vd)  # noqa: E731
@@ -224,7 +236,7 @@ def main():
         dense["own_kernel_all_blocks_ms"] = round(full_ms, 4)
         dense["own_kernel_all_blocks_tflops"] = round(full_flops / (full_ms * 1e-3) / 1e12, 2)
     if fp8:
-        kname = "bsa_fwd_dma_kernel<bf16,128,e4m3>"
+        kname = "bsa_fwd_dma_kernel<bf16,128,gather,e4m3>" if fused else "bsa_fwd_dma_kernel<bf16,128,e4m3>"
     elif fused:
         kname = "bsa_fwd_dma_kernel<bf16,128,gather>"
     elif D == 128 and bs in (64, 128):
@@ -234,8 +246,11 @@ def main():
 
     # Bytes the call moves outside attention: the pools read Q and K once
     # (fused); the tiled sequence also writes and re-reads the tiles and untiles.
-    if fused:
+    if fused and not fp8:
         prep_bytes = 2.0 * (wl.lq + wl.lk) * H * D * B
+    elif fp8 and fused:
+        # Q, K read as bf16 and written as e4m3 tiles (V and O stay in token order).
+        prep_bytes = (2.0 * (wl.lq + wl.lk) + 1.0 * (g.nq_blk + g.nk_blk) * bs) * H * D * B
     elif fp8:
         # Q, K read as bf16 and written as e4m3 tiles; V gathered; output untiled.
         prep_bytes = (2.0 * (wl.lq + 2 * wl.lk) + 1.0 * (g.nq_blk + g.nk_blk) * bs + 2.0 * g.nk_blk * bs
@@ -269,6 +284,7 @@ def main():
                              "pct_bf16_peak": round(100.0 * attn_tflops / PEAK_BF16_TFLOPS, 2),
                              "retained_gflop": round(flops / 1e9, 2)},
         ("attention_kernel_bf16" if fp8 else "attention_kernel_tiled"): tiled_info,
+        "attention_kernel_e4m3_tiled": tiled_fp8_info,
         "dense_comparator": dense,
         "roofline": {"bound": "mfma", "kernel": kname,
                      "achieved": round(attn_tflops, 2), "peak": round(peak, 1), "unit": "TFLOP/s",
@@ -303,22 +319,26 @@ def profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params
     src = torch.empty(1 << 27, dtype=torch.bfloat16, device=dev).fill_(1.0)   # 256 MiB
     dst = torch.empty_like(src)
     fp8 = fp8_tiles is not None
-    fused = _pipeline.uses_fused(qd, kd, vd, wl.tile, wl.latent_hw) and not fp8
+    fused = _pipeline.uses_fused(qd, kd, vd, wl.tile, wl.latent_hw)
     balance = _pipeline.ragged(params)
     q_pool = torch.empty_like(q_p)
     k_pool = torch.empty_like(k_p)
     for _ in range(args.steps):
         if fp8:
-            # The e4m3 call's kernels: quantizing Q gather + pool, quantizing K
-            # gather + V gather + K pool, block mask, e4m3 attention (+ merge),
-            # untile; then the bf16 tiled attention on the same lists.
+            # The fused e4m3 call's kernels: quantizing Q gather + pool,
+            # quantizing K gather + pool, block mask, e4m3 attention reading V
+            # and writing O in token order (+ merge); then, on the same lists,
+            # the tiled e4m3 attention (V tiles from a K/V gather) and the bf16
+            # tiled attention.
             q8, qs, k8, ks = fp8_tiles
             _core.tile_prep_fp8(qd, q8, qs, q_pool, 0, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
-            _core.kv_prep_fp8(kd, vd, k8, ks, v_all, k_pool, 0, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+            _core.tile_prep_fp8(kd, k8, ks, k_pool, 0, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
             fast_generate_indices(q_pool, k_pool, 0, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), params, dev)
+            _core.bsa_forward_fp8_gather(q8.flatten(2, 3), qs, k8.flatten(2, 3), ks, vd, None, 0, g.T_q, g.T_k, g.H,
+                                         g.W, g.tt, g.th, g.tw, g.nh, g.nw, ind, cnt, scale, o_tok, balance=balance)
+            _core.kv_prep_fp8(kd, vd, k8, ks, v_all, k_pool, 0, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
             _core.bsa_forward_fp8(q8.flatten(2, 3), qs, k8.flatten(2, 3), ks, vf, ind, cnt, scale, bs, out=out,
                                   balance=balance)
-            _core.untile(out.view(B, H, g.nq_blk, bs, D), o_lin, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
             _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs, out=out, balance=balance)
         elif fused:
             # The call's own kernels: Q pool, K pool, block mask, fused
@@ -348,10 +368,11 @@ def profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params
     }
     if fp8:
         alg["bsa_fwd_kernel"]["bytes_min_e4m3"] = (1 * (g.nq_blk + g.nk_blk) + 2 * g.nk_blk + 2 * g.nq_blk) * bs * H * D * B
+        alg["bsa_fwd_kernel"]["bytes_min_e4m3_fused"] = ((g.nq_blk + g.nk_blk) * bs + 2 * (wl.lk + wl.lq)) * H * D * B
         alg["gather_fp8_kernel<1> (Q)"] = {"bytes": H * D * B * (e * wl.lq + g.nq_blk * bs) + e * H * D * g.nq_blk}
+        alg["gather_fp8_kernel<1> (K)"] = {"bytes": H * D * B * (e * wl.lk + g.nk_blk * bs) + e * H * D * g.nk_blk}
         alg["gather_fp8_kernel<2> (K e4m3, V)"] = {"bytes": H * D * B * (2 * e * wl.lk + (1 + e) * g.nk_blk * bs)
                                                    + e * H * D * g.nk_blk}
-        alg["untile_kernel"] = {"bytes": e * H * D * B * 2 * wl.lq}
     elif fused:
         alg["bsa_fwd_kernel"]["bytes_min_fused"] = e * (2 * wl.lq + 2 * wl.lk) * H * D * B
         alg["pool (Q)"] = {"bytes": e * H * D * B * wl.lq + e * H * D * g.nq_blk, "grid_blocks": g.nq_blk}

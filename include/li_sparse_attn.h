@@ -314,6 +314,26 @@ int li_bsa_fwd_fp8(int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int32_t D,
                    float sm_scale, int32_t block_size,
                    void* out, float* lse, void* workspace, int64_t workspace_bytes, int32_t flags, void* stream);
 
+/*
+ * li_bsa_fwd_fp8 with V read and O written in token order, as
+ * li_bsa_fwd_gather does (the fused call of the e4m3 variant):
+ *   q8 (B, NH, nq_blk*128, D) e4m3 tiles, q_scale (B, NH, nq_blk) fp32
+ *   k8 (B, NH, (num_txt_blk + nk_blk)*128, D) e4m3 tiles (text blocks
+ *     first), k_scale (B, NH, num_txt_blk + nk_blk) fp32; all contiguous
+ *   v (B, NH, Lk, D) bf16 token view and v_txt / num_txt_blk, the q_geom /
+ *     k_geom grids, the lists, out (B, NH, Lq, D) bf16 token view, lse,
+ *     workspace and flags: as for li_bsa_fwd_gather (the same shape limits).
+ * Same results as li_bsa_fwd_fp8 on the V tiles followed by li_untile.
+ */
+int li_bsa_fwd_fp8_gather(int32_t B, int32_t NH, int32_t D,
+                          const void* q8, const float* q_scale, const void* k8, const float* k_scale,
+                          const void* v, const int64_t v_strides[4], const void* v_txt, int32_t num_txt_blk,
+                          const li_tile_geom* q_geom, const li_tile_geom* k_geom,
+                          const int32_t* block_indices, const int64_t idx_strides[4], int32_t n_cols,
+                          const int32_t* block_counts, const int64_t cnt_strides[3],
+                          float sm_scale, void* out, const int64_t out_strides[4], float* lse,
+                          void* workspace, int64_t workspace_bytes, int32_t flags, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -424,7 +424,8 @@ __device__ __forceinline__ void sched_m_phase() {
 // k_scale) and S^T = K Q^T is taken with the 32x32x64 e4m3 MFMA (four per
 // block and wave instead of sixteen); the block's score scale
 // qk_scale * q_scale * k_scale[blk] enters the softmax, and P V stays in
-// 16-bit.  The e4m3 K stage has 128-byte rows with no padding: the 16-byte
+// 16-bit.  Q and K are always tiled (text blocks included); with G, V is
+// read and O written in token order.  The e4m3 K stage has 128-byte rows with no padding: the 16-byte
 // granule g of row r sits at slot g ^ ((r >> 1) & 7), so the 16 rows a
 // 16-lane group reads (any 16 aligned rows) fall in 16 distinct bank windows.
 // DN (dense calls, token-order addressing only): no index lists, every tile
@@ -434,8 +435,8 @@ template <typename E, int BS, bool G = false, bool F8 = false, bool DN = false>
 __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   using C = DmaCfg<BS>;
   static_assert(!G || BS == 128, "token-order addressing is built for 128-row tiles");
-  static_assert(!F8 || (BS == 128 && !G), "the e4m3 kernel is built for tiled 128-row blocks");
-  static_assert(!DN || G, "dense calls use token-order addressing");
+  static_assert(!F8 || BS == 128, "the e4m3 kernel is built for 128-row blocks");
+  static_assert(!DN || (G && !F8), "dense calls use token-order addressing and 16-bit keys");
   constexpr int D = 128;
   typedef typename E::vec8 vec8;
   typedef __attribute__((address_space(3))) void lds_void;
@@ -817,7 +818,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
         uint32_t ft, fh, fw;
         coords(gw * LPW + j, ft, fh, fw);
         const uint32_t coff = (ft * a.g.H + fh) * a.g.W + fw;
-        kvo[j] = coff * (uint32_t)(2 * a.g.ks[2]) + k_src_vis - (j & 3) * 1024;
+        if constexpr (!F8) kvo[j] = coff * (uint32_t)(2 * a.g.ks[2]) + k_src_vis - (j & 3) * 1024;
         vvo[j] = coff * (uint32_t)(2 * a.g.vs[2]) + v_src_vis - (j & 3) * 1024;
       }
       coords(lane & 31, lane_ft, lane_fh, lane_fw);
@@ -865,6 +866,10 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
         s_.alt = is_v ? reinterpret_cast<const char*>(vhead + (int64_t)g_.blk * BS * D) + gw * LPW * 1024
                       : kbytes + (int64_t)g_.blk * BS * D * KEB + gw * KPW * 1024;
       } else {
+        if (F8 && !is_v) {
+          s_.alt = kbytes + (int64_t)g_.blk * BS * D + gw * KPW * 1024;
+          return s_;
+        }
         s_.vis = (is_v ? vis_v : vis_k) + (uint64_t)(uint32_t)g_.l0 * (is_v ? vst : kst);
         s_.mask = g_.mask;
         const char* tb = (is_v ? txt_v : txt_k) + (int64_t)g_.blk * (BS * D * 2);
@@ -880,7 +885,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       const Blk& s_ = isv ? sv : sk;
       const uint32_t lin = isv ? v_src : (F8 ? k8_src[j & 1] : k_src);
       const char* alt = j < 4 ? s_.alt : s_.alt + 4096;
-      if constexpr (!G)
+      if (!G || (F8 && !isv))
         return DmaSrc{alt, lin};
       else
         return dma_sel(s_.mask, j, s_.vis, isv ? vvo[j] : kvo[j], alt, lin);
@@ -1241,12 +1246,13 @@ int launch_bsa_gather(BsaArgs& a, int tiles, hipStream_t s) {
   return launch_status();
 }
 
+template <bool G>
 int launch_bsa_fp8(BsaArgs& a, int tiles, hipStream_t s) {
   const int nsplit = tiles - a.n_full;
   clear_launch_error();
-  hipLaunchKernelGGL((bsa_fwd_dma_kernel<Bf16, 128, false, true>), dim3(a.n_full + 2 * nsplit),
-                     dim3(DmaCfg<128>::NTHR), 0, s, a);
-  if (nsplit > 0) hipLaunchKernelGGL(bsa_merge_kernel<Bf16>, dim3(4 * nsplit), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((bsa_fwd_dma_kernel<Bf16, 128, G, true>), dim3(a.n_full + 2 * nsplit), dim3(DmaCfg<128>::NTHR),
+                     0, s, a);
+  if (nsplit > 0) hipLaunchKernelGGL((bsa_merge_kernel<Bf16, G>), dim3(4 * nsplit), dim3(256), 0, s, a);
   return launch_status();
 }
 
@@ -1459,21 +1465,22 @@ bool row_view_ok(const void* p, const int64_t st[4]) {
   return p && aligned16(p) && st[3] == 1 && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 && st[2] > 0;
 }
 
-}  // namespace
-
-extern "C" int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D, const void* q,
-                                 const int64_t q_strides[4], const void* k, const int64_t k_strides[4],
-                                 const void* v, const int64_t v_strides[4], const void* k_txt, const void* v_txt,
-                                 int32_t num_txt_blk, const li_tile_geom* q_geom, const li_tile_geom* k_geom,
-                                 const int32_t* block_indices, const int64_t idx_strides[4], int32_t n_cols,
-                                 const int32_t* block_counts, const int64_t cnt_strides[3], float sm_scale, void* out,
-                                 const int64_t out_strides[4], float* lse, void* workspace, int64_t workspace_bytes,
-                                 int32_t flags, void* stream) {
-  if (!q_strides || !k_strides || !v_strides || !out_strides || !q_geom || !k_geom || !block_indices ||
-      !idx_strides || !block_counts || !cnt_strides)
+// Checks and BsaArgs of a token-order (fused) call over the q_geom / k_geom
+// grids.  With e4m3 keys (k8) only V is read in token order: k / k_strides
+// are unused and K comes from the tiles in a.k.  Returns LI_OK with `tiles`
+// set, or a status; tiles = 0 means nothing to launch.
+int gather_setup(BsaArgs& a, int64_t& tiles, int32_t B, int32_t NH, int32_t D, const void* q,
+                 const int64_t q_strides[4], const void* k, const int64_t k_strides[4], const void* v,
+                 const int64_t v_strides[4], const void* k_txt, const void* v_txt, int32_t num_txt_blk,
+                 const li_tile_geom* q_geom, const li_tile_geom* k_geom, const int32_t* block_indices,
+                 const int64_t idx_strides[4], int32_t n_cols, const int32_t* block_counts,
+                 const int64_t cnt_strides[3], float sm_scale, void* out, const int64_t out_strides[4], float* lse,
+                 bool k8) {
+  tiles = 0;
+  if (!v_strides || !out_strides || !q_geom || !k_geom || !block_indices || !idx_strides || !block_counts ||
+      !cnt_strides || (!k8 && (!q_strides || !k_strides)))
     return LI_ERR_INVALID_ARG;
   if (B <= 0 || NH <= 0 || n_cols < 0 || num_txt_blk < 0) return LI_ERR_INVALID_ARG;
-  if (dtype != LI_DTYPE_BF16 && dtype != LI_DTYPE_F16) return LI_ERR_UNSUPPORTED;
   const li_tile_geom& gq = *q_geom;
   const li_tile_geom& gk = *k_geom;
   if (gq.H != gk.H || gq.W != gk.W || gq.tt != gk.tt || gq.th != gk.th || gq.tw != gk.tw || gq.nh != gk.nh ||
@@ -1489,11 +1496,12 @@ extern "C" int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D, co
   // overlap, so a chunk's byte offset from its tile's origin is at least
   // 1024 * (chunk index) (the kernel subtracts the instruction offset).
   if (gq.H < gq.th || gq.W < gq.tw) return LI_ERR_UNSUPPORTED;
-  if (!row_view_ok(q, q_strides) || !row_view_ok(k, k_strides) || !row_view_ok(v, v_strides) ||
+  if ((!k8 && (!row_view_ok(q, q_strides) || !row_view_ok(k, k_strides))) || !row_view_ok(v, v_strides) ||
       !row_view_ok(out, out_strides))
     return LI_ERR_INVALID_ARG;
-  if (k_strides[2] < D || v_strides[2] < D) return LI_ERR_UNSUPPORTED;
-  if (num_txt_blk > 0 && (!k_txt || !v_txt || !aligned16(k_txt) || !aligned16(v_txt))) return LI_ERR_INVALID_ARG;
+  if ((!k8 && k_strides[2] < D) || v_strides[2] < D) return LI_ERR_UNSUPPORTED;
+  if (num_txt_blk > 0 && (!v_txt || !aligned16(v_txt) || (!k8 && (!k_txt || !aligned16(k_txt)))))
+    return LI_ERR_INVALID_ARG;
   const int64_t nq = (int64_t)((gq.T + gq.tt - 1) / gq.tt) * gq.nh * gq.nw;
   const int64_t nkv = (int64_t)((gk.T + gk.tt - 1) / gk.tt) * gk.nh * gk.nw;
   if ((int64_t)gq.nh * gq.nw >= 65536 || nkv + num_txt_blk >= 65536 || nq >= 65536) return LI_ERR_SHAPE;
@@ -1501,12 +1509,11 @@ extern "C" int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D, co
   // The byte offset of a K/V row from its tile's origin token is held in 32
   // bits: at most max_row tokens, times the token stride, plus one row.
   const int64_t max_row = (int64_t)(gq.tt - 1) * gq.H * gq.W + (int64_t)(gq.th - 1) * gq.W + gq.tw - 1;
-  const int64_t kv_st = k_strides[2] > v_strides[2] ? k_strides[2] : v_strides[2];
+  const int64_t kv_st = !k8 && k_strides[2] > v_strides[2] ? k_strides[2] : v_strides[2];
   if ((max_row * kv_st + D) * 2 > (1ll << 32)) return LI_ERR_SHAPE;
   if (nq == 0) return LI_OK;
-  const int64_t tiles = nq * B * NH;
+  tiles = nq * B * NH;
   if (tiles > 0x7FFFFFFF) return LI_ERR_SHAPE;
-  BsaArgs a = {};
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
   a.v = static_cast<const uint16_t*>(v);
@@ -1524,8 +1531,8 @@ extern "C" int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D, co
   a.qk_scale = sm_scale * 1.44269504f;
   BsaGather& g = a.g;
   for (int i = 0; i < 3; ++i) {
-    g.qs[i] = q_strides[i];
-    g.ks[i] = k_strides[i];
+    g.qs[i] = k8 ? 0 : q_strides[i];
+    g.ks[i] = k8 ? v_strides[i] : k_strides[i];
     g.vs[i] = v_strides[i];
     g.os[i] = out_strides[i];
   }
@@ -1551,8 +1558,28 @@ extern "C" int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D, co
   g.k_tokens = gk.T * gk.H * gk.W;
   g.txt_tail = 0;
   g.vis_tail = 0;
+  return LI_OK;
+}
+
+}  // namespace
+
+extern "C" int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D, const void* q,
+                                 const int64_t q_strides[4], const void* k, const int64_t k_strides[4],
+                                 const void* v, const int64_t v_strides[4], const void* k_txt, const void* v_txt,
+                                 int32_t num_txt_blk, const li_tile_geom* q_geom, const li_tile_geom* k_geom,
+                                 const int32_t* block_indices, const int64_t idx_strides[4], int32_t n_cols,
+                                 const int32_t* block_counts, const int64_t cnt_strides[3], float sm_scale, void* out,
+                                 const int64_t out_strides[4], float* lse, void* workspace, int64_t workspace_bytes,
+                                 int32_t flags, void* stream) {
+  if (dtype != LI_DTYPE_BF16 && dtype != LI_DTYPE_F16) return LI_ERR_UNSUPPORTED;
+  BsaArgs a = {};
+  int64_t tiles = 0;
+  int st = gather_setup(a, tiles, B, NH, D, q, q_strides, k, k_strides, v, v_strides, k_txt, v_txt, num_txt_blk,
+                        q_geom, k_geom, block_indices, idx_strides, n_cols, block_counts, cnt_strides, sm_scale, out,
+                        out_strides, lse, false);
+  if (st != LI_OK || tiles == 0) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int st = plan_units(a, tiles, D, 128, workspace, workspace_bytes, flags, s);
+  st = plan_units(a, tiles, D, 128, workspace, workspace_bytes, flags, s);
   if (st != LI_OK) return st;
   if (dtype == LI_DTYPE_BF16) return launch_bsa_gather<Bf16>(a, (int)tiles, s);
   return launch_bsa_gather<F16>(a, (int)tiles, s);
@@ -1598,7 +1625,32 @@ extern "C" int li_bsa_fwd_fp8(int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int st = plan_units(a, tiles, D, block_size, workspace, workspace_bytes, flags, s);
   if (st != LI_OK) return st;
-  return launch_bsa_fp8(a, (int)tiles, s);
+  return launch_bsa_fp8<false>(a, (int)tiles, s);
+}
+
+extern "C" int li_bsa_fwd_fp8_gather(int32_t B, int32_t NH, int32_t D, const void* q8, const float* q_scale,
+                                     const void* k8, const float* k_scale, const void* v, const int64_t v_strides[4],
+                                     const void* v_txt, int32_t num_txt_blk, const li_tile_geom* q_geom,
+                                     const li_tile_geom* k_geom, const int32_t* block_indices,
+                                     const int64_t idx_strides[4], int32_t n_cols, const int32_t* block_counts,
+                                     const int64_t cnt_strides[3], float sm_scale, void* out,
+                                     const int64_t out_strides[4], float* lse, void* workspace,
+                                     int64_t workspace_bytes, int32_t flags, void* stream) {
+  if (!q8 || !q_scale || !k8 || !k_scale || !aligned16(q8) || !aligned16(k8) ||
+      ((reinterpret_cast<uintptr_t>(q_scale) | reinterpret_cast<uintptr_t>(k_scale)) & 3u))
+    return LI_ERR_INVALID_ARG;
+  BsaArgs a = {};
+  int64_t tiles = 0;
+  int st = gather_setup(a, tiles, B, NH, D, q8, nullptr, k8, nullptr, v, v_strides, nullptr, v_txt, num_txt_blk,
+                        q_geom, k_geom, block_indices, idx_strides, n_cols, block_counts, cnt_strides, sm_scale, out,
+                        out_strides, lse, true);
+  if (st != LI_OK || tiles == 0) return st;
+  a.q_scale = q_scale;
+  a.k_scale = k_scale;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  st = plan_units(a, tiles, D, 128, workspace, workspace_bytes, flags, s);
+  if (st != LI_OK) return st;
+  return launch_bsa_fp8<true>(a, (int)tiles, s);
 }
 
 extern "C" int li_attn_fwd_dense(int dtype, int32_t B, int32_t NH, int32_t D, int32_t Lq, int32_t Lk, const void* q,

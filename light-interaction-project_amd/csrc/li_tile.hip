@@ -59,8 +59,12 @@ __device__ __forceinline__ void store8(uint16_t* p, int64_t stride, bool vec, u3
   }
 }
 
-template <typename E, int D, int NT>
-__global__ __launch_bounds__(256) void gather_pool_kernel(GatherArgs a) {
+// VEC: every row of the source and the tiles is moved with 16-byte vector
+// accesses (unit innermost stride, 16-byte aligned rows).  The element-wise
+// path for other strides is a separate instantiation, so the vector one does
+// not carry its per-element address registers.
+template <typename E, int D, int NT, bool VEC>
+__global__ __launch_bounds__(256, VEC ? 4 : 1) void gather_pool_kernel(GatherArgs a) {
   constexpr int CPR = D / 8;
   constexpr int NG = 256 / CPR;
   __shared__ float red[NG][D];
@@ -73,7 +77,7 @@ __global__ __launch_bounds__(256) void gather_pool_kernel(GatherArgs a) {
   const li_tile_geom& g = a.g;
   const int cw = blk % g.nw, rem = blk / g.nw;
   const int ch = rem % g.nh, ct = rem / g.nh;
-  const bool vs = a.vec_src != 0, vd = a.vec_dst != 0;
+  const bool vs = VEC || a.vec_src != 0, vd = VEC || a.vec_dst != 0;
 
   // NT tensors gathered into tiles (the first one also pooled); NT = 0 pools
   // tensor 0 without writing tiles.
@@ -154,8 +158,8 @@ __global__ __launch_bounds__(256) void gather_pool_kernel(GatherArgs a) {
 // copied unquantized) are as in gather_pool_kernel.  The whole block is held
 // in registers (BS <= 8 NG rows): loads, then the workgroup's amax, then the
 // stores.
-template <typename E, int D, int NT>
-__global__ __launch_bounds__(256) void gather_fp8_kernel(GatherArgs a) {
+template <typename E, int D, int NT, bool VEC>
+__global__ __launch_bounds__(256, VEC ? 4 : 1) void gather_fp8_kernel(GatherArgs a) {
   constexpr int CPR = D / 8;
   constexpr int NG = 256 / CPR;
   constexpr int R = 8;
@@ -170,7 +174,7 @@ __global__ __launch_bounds__(256) void gather_fp8_kernel(GatherArgs a) {
   const li_tile_geom& g = a.g;
   const int cw = blk % g.nw, rem = blk / g.nw;
   const int ch = rem % g.nh, ct = rem / g.nh;
-  const bool vs = a.vec_src != 0, vd = a.vec_dst != 0;
+  const bool vs = VEC || a.vec_src != 0, vd = VEC || a.vec_dst != 0;
 
   const uint16_t* sbase[NT];
 #pragma unroll
@@ -274,7 +278,7 @@ struct UntileArgs {
   int32_t vec_src, vec_dst;
 };
 
-template <int D>
+template <int D, bool VEC>
 __global__ __launch_bounds__(256) void untile_kernel(UntileArgs a) {
   constexpr int CPR = D / 8;
   constexpr int NG = 256 / CPR;
@@ -286,7 +290,7 @@ __global__ __launch_bounds__(256) void untile_kernel(UntileArgs a) {
   const li_tile_geom& g = a.g;
   const int cw = blk % g.nw, rem = blk / g.nw;
   const int ch = rem % g.nh, ct = rem / g.nh;
-  const bool vs = a.vec_src != 0, vd = a.vec_dst != 0;
+  const bool vs = VEC || a.vec_src != 0, vd = VEC || a.vec_dst != 0;
   const uint16_t* sbase = a.src + b * a.ss[0] + h * a.ss[1] + blk * a.ss[2] + (int64_t)(8 * c) * a.ss[4];
   uint16_t* dbase = a.dst + b * a.ds[0] + h * a.ds[1] + (int64_t)(8 * c) * a.ds[3];
   for (int f = g0; f < a.bs; f += NG) {
@@ -340,29 +344,47 @@ int launch_gather(int dtype, int32_t B, int32_t NH, int32_t D, GatherArgs& a, co
     // The block is held in registers: at most 8 rows per thread.
     if (a.bs > 8 * (256 / (D / 8))) return LI_ERR_UNSUPPORTED;
     clear_launch_error();
+    const bool vec = a.vec_src && (NT < 2 || a.vec_dst);
+#define LI_FP8_LAUNCH(E_, D_)                                                                   \
+  do {                                                                                         \
+    if (vec)                                                                                   \
+      hipLaunchKernelGGL((gather_fp8_kernel<E_, D_, NT, true>), grid, dim3(256), 0, stream, a);  \
+    else                                                                                       \
+      hipLaunchKernelGGL((gather_fp8_kernel<E_, D_, NT, false>), grid, dim3(256), 0, stream, a); \
+  } while (0)
     if (dtype == LI_DTYPE_BF16 && D == 128)
-      hipLaunchKernelGGL((gather_fp8_kernel<Bf16, 128, NT>), grid, dim3(256), 0, stream, a);
+      LI_FP8_LAUNCH(Bf16, 128);
     else if (dtype == LI_DTYPE_BF16 && D == 64)
-      hipLaunchKernelGGL((gather_fp8_kernel<Bf16, 64, NT>), grid, dim3(256), 0, stream, a);
+      LI_FP8_LAUNCH(Bf16, 64);
     else if (dtype == LI_DTYPE_F16 && D == 128)
-      hipLaunchKernelGGL((gather_fp8_kernel<F16, 128, NT>), grid, dim3(256), 0, stream, a);
+      LI_FP8_LAUNCH(F16, 128);
     else if (dtype == LI_DTYPE_F16 && D == 64)
-      hipLaunchKernelGGL((gather_fp8_kernel<F16, 64, NT>), grid, dim3(256), 0, stream, a);
+      LI_FP8_LAUNCH(F16, 64);
     else
       return LI_ERR_UNSUPPORTED;
+#undef LI_FP8_LAUNCH
     return launch_status();
   }
   clear_launch_error();
+  const bool vec = a.vec_src && (NT == 0 || a.vec_dst);
+#define LI_GATHER_LAUNCH(E_, D_)                                                                 \
+  do {                                                                                          \
+    if (vec)                                                                                    \
+      hipLaunchKernelGGL((gather_pool_kernel<E_, D_, NT, true>), grid, dim3(256), 0, stream, a);  \
+    else                                                                                        \
+      hipLaunchKernelGGL((gather_pool_kernel<E_, D_, NT, false>), grid, dim3(256), 0, stream, a); \
+  } while (0)
   if (dtype == LI_DTYPE_BF16 && D == 128)
-    hipLaunchKernelGGL((gather_pool_kernel<Bf16, 128, NT>), grid, dim3(256), 0, stream, a);
+    LI_GATHER_LAUNCH(Bf16, 128);
   else if (dtype == LI_DTYPE_BF16 && D == 64)
-    hipLaunchKernelGGL((gather_pool_kernel<Bf16, 64, NT>), grid, dim3(256), 0, stream, a);
+    LI_GATHER_LAUNCH(Bf16, 64);
   else if (dtype == LI_DTYPE_F16 && D == 128)
-    hipLaunchKernelGGL((gather_pool_kernel<F16, 128, NT>), grid, dim3(256), 0, stream, a);
+    LI_GATHER_LAUNCH(F16, 128);
   else if (dtype == LI_DTYPE_F16 && D == 64)
-    hipLaunchKernelGGL((gather_pool_kernel<F16, 64, NT>), grid, dim3(256), 0, stream, a);
+    LI_GATHER_LAUNCH(F16, 64);
   else
     return LI_ERR_UNSUPPORTED;
+#undef LI_GATHER_LAUNCH
   return launch_status();
 }
 
@@ -463,10 +485,15 @@ extern "C" int li_untile(int dtype, int32_t B, int32_t NH, int32_t D, const void
   dim3 grid((unsigned)nblk, (unsigned)(B * NH));
   hipStream_t s = static_cast<hipStream_t>(stream);
   clear_launch_error();
-  if (D == 128)
-    hipLaunchKernelGGL(untile_kernel<128>, grid, dim3(256), 0, s, a);
+  const bool vec = a.vec_src && a.vec_dst;
+  if (D == 128 && vec)
+    hipLaunchKernelGGL((untile_kernel<128, true>), grid, dim3(256), 0, s, a);
+  else if (D == 128)
+    hipLaunchKernelGGL((untile_kernel<128, false>), grid, dim3(256), 0, s, a);
+  else if (D == 64 && vec)
+    hipLaunchKernelGGL((untile_kernel<64, true>), grid, dim3(256), 0, s, a);
   else if (D == 64)
-    hipLaunchKernelGGL(untile_kernel<64>, grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((untile_kernel<64, false>), grid, dim3(256), 0, s, a);
   else
     return LI_ERR_UNSUPPORTED;
   return launch_status();

@@ -449,6 +449,49 @@ def bsa_forward_fp8(q8, q_scale, k8, k_scale, v, indices, counts, sm_scale, bloc
     return (out, lse) if return_lse else out
 
 
+def bsa_forward_fp8_gather(q8, q_scale, k8, k_scale, v, v_txt, num_txt_blk, T_q, T_k, H, W, tt, th, tw, nh, nw,
+                           indices, counts, sm_scale, out, return_lse=False, balance=False):
+    """e4m3 attention with V read and O written in token order (see li_bsa_fwd_fp8_gather).
+
+    q8 (B,NH,nq_blk*128,D) / k8 (B,NH,(num_txt_blk+nk_blk)*128,D) e4m3 tiles with their (B,NH,nblk) scales;
+    v (B,NH,Lk,D) bf16 token view; v_txt (B,NH,num_txt_blk*128,D) contiguous zero-padded or None;
+    out (B,NH,Lq,D) bf16 token view, written at valid tokens.
+    """
+    dev = _device_check(q8, q_scale, k8, k_scale, v, indices, counts, out)
+    if q8.dtype != FP8 or k8.dtype != FP8 or v.dtype != torch.bfloat16 or out.dtype != torch.bfloat16:
+        raise TypeError("q8/k8 must be float8_e4m3fn, v and out bfloat16")
+    if not (q8.is_contiguous() and k8.is_contiguous() and q_scale.is_contiguous() and k_scale.is_contiguous()):
+        raise ValueError("the e4m3 tiles and scales must be contiguous")
+    B, NH, _, D = v.shape
+    nq, nk = num_blocks(T_q, tt, nh, nw), num_blocks(T_k, tt, nh, nw)
+    if tuple(q8.shape) != (B, NH, nq * 128, D) or tuple(q_scale.shape) != (B, NH, nq):
+        raise ValueError(f"q8 {tuple(q8.shape)} / q_scale {tuple(q_scale.shape)} do not hold {nq} tiles")
+    nkb = num_txt_blk + nk
+    if tuple(k8.shape) != (B, NH, nkb * 128, D) or tuple(k_scale.shape) != (B, NH, nkb):
+        raise ValueError(f"k8 {tuple(k8.shape)} / k_scale {tuple(k_scale.shape)} do not hold {nkb} blocks")
+    if indices.dtype != torch.int32 or counts.dtype != torch.int32:
+        raise TypeError("block indices and counts must be int32")
+    if num_txt_blk > 0 and (v_txt is None or not v_txt.is_contiguous()
+                            or tuple(v_txt.shape) != (B, NH, num_txt_blk * 128, D)):
+        raise ValueError("v_txt must be a contiguous (B, NH, num_txt_blk*128, D) buffer")
+    gq = TileGeom(T_q, H, W, tt, th, tw, nh, nw)
+    gk = TileGeom(T_k, H, W, tt, th, tw, nh, nw)
+    lse = torch.empty((B, NH, nq * 128), dtype=torch.float32, device=dev) if return_lse else None
+    with torch.cuda.device(dev):
+        ws_bytes = int(lib.li_bsa_fwd_workspace_size(B, NH, nq * 128, D, 128))
+    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev) if ws_bytes > 0 else None
+    st = lib.li_bsa_fwd_fp8_gather(B, NH, D, q8.data_ptr(), q_scale.data_ptr(), k8.data_ptr(), k_scale.data_ptr(),
+                                   v.data_ptr(), i64_array(v.stride()),
+                                   v_txt.data_ptr() if v_txt is not None else None, int(num_txt_blk),
+                                   ctypes.byref(gq), ctypes.byref(gk), indices.data_ptr(), i64_array(indices.stride()),
+                                   indices.shape[3], counts.data_ptr(), i64_array(counts.stride()), float(sm_scale),
+                                   out.data_ptr(), i64_array(out.stride()), lse.data_ptr() if lse is not None else None,
+                                   ws.data_ptr() if ws is not None else None, ws_bytes,
+                                   _lib.LI_BSA_BALANCE if balance else 0, _stream(dev))
+    check("li_bsa_fwd_fp8_gather", st)
+    return (out, lse) if return_lse else out
+
+
 def dense_supported(q, k, v, k_txt=None):
     """Inputs li_attn_fwd_dense takes: fp16/bf16, D = 128, Lk a multiple of 4, token views with unit d stride,
     8-element-multiple strides, 16-byte aligned, K/V token strides >= D."""

@@ -163,6 +163,45 @@ def _tiled_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, ev
     return o_out if o_out.dtype == out_dtype else o_out.to(out_dtype)
 
 
+def _fused_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance):
+    """e4m3 Q/K tiles from the quantizing gathers, then one kernel that reads V and writes O in token order."""
+    B, NH, _, D = q.shape
+    dev = q.device
+    f8 = _core.FP8
+    _stage(events, "alloc_start")
+    q8 = torch.empty((B, NH, g.nq_blk, g.bs, D), device=dev, dtype=f8)
+    q_scale = torch.empty((B, NH, g.nq_blk), device=dev, dtype=torch.float32)
+    q_pool = torch.empty((B, NH, g.nq_blk, D), device=dev, dtype=q.dtype)
+    nkb = g.num_txt_blk + g.nk_blk
+    k8 = torch.empty((B, NH, nkb, g.bs, D), device=dev, dtype=f8)
+    k_scale = torch.empty((B, NH, nkb), device=dev, dtype=torch.float32)
+    k_pool = torch.empty((B, NH, g.nk_blk, D), device=dev, dtype=q.dtype)
+    vt = None
+    if text_len > 0:
+        pad = g.num_txt_blk * g.bs - text_len
+        kt = F.pad(k_txt, (0, 0, 0, pad)) if pad > 0 else k_txt
+        vt = (F.pad(v_txt, (0, 0, 0, pad)) if pad > 0 else v_txt).contiguous()
+    o_out = torch.empty_like(q)
+    _stage(events, "alloc_end")
+    _stage(events, "prep_start")
+    if text_len > 0:
+        _core.tile_prep_fp8(kt, k8, k_scale, None, 0, 0, g.num_txt_blk, 1, g.bs, 1, 1, g.bs, 1, 1)
+    _core.tile_prep_fp8(q, q8, q_scale, q_pool, 0, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    _core.tile_prep_fp8(k_vis, k8, k_scale, k_pool, g.num_txt_blk, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    _stage(events, "prep_end")
+    _stage(events, "index_start")
+    indices, counts = select(q_pool, k_pool, text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
+    _stage(events, "index_end")
+    _stage(events, "attn_start")
+    _core.bsa_forward_fp8_gather(q8.flatten(2, 3), q_scale, k8.flatten(2, 3), k_scale, v_vis, vt, g.num_txt_blk,
+                                 g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw, indices, counts,
+                                 1.0 / math.sqrt(D), o_out, balance=balance)
+    _stage(events, "attn_end")
+    _stage(events, "untile_start")
+    _stage(events, "untile_end")
+    return o_out if o_out.dtype == out_dtype else o_out.to(out_dtype)
+
+
 def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, events=None, fused=True,
                      balance=False, qk_fp8=False):
     """One sparse-attention forward.
@@ -191,6 +230,8 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
         if dt != torch.bfloat16 or not fp8_supported(D, tile):
             raise ValueError(f"qk_fp8 is built for bfloat16, D = 128 and 128-token tiles (got {dt}, D = {D}, "
                              f"tile {tuple(tile)})")
+        if fused and uses_fused(q, k_vis, v_vis, tile, (g.H, g.W)):
+            return _fused_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance)
         return _tiled_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance)
     if fused and uses_fused(q, k_vis, v_vis, tile, (g.H, g.W)):
         return _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance)

@@ -253,3 +253,31 @@ def test_fp8_rejects_unsupported(dev):
                               torch.ones((1, 1, 4), device=dev), x["v"].to(dev),
                               torch.zeros((1, 1, 2, 1), dtype=torch.int32, device=dev),
                               torch.ones((1, 1, 2), dtype=torch.int32, device=dev), 0.1, 64)
+
+
+@pytest.mark.parametrize("latent_hw,tile,frames_k,text,layout", [((30, 52), (2, 8, 8), 8, 200, "blhd"),
+                                                                  ((22, 40), (4, 4, 8), 8, 0, "bhld"),
+                                                                  ((30, 52), (2, 8, 8), 12, 130, "bhld")])
+def test_fp8_fused_equals_tiled(dev, latent_hw, tile, frames_k, text, layout):
+    """The fused e4m3 call (V read, O written in token order) gives the bits of the tiled e4m3 sequence."""
+    from li_sparse import _pipeline
+    from li_sparse.hy.ar_sparse_operation import fast_generate_indices
+
+    wl = Workload("fp8_fused", 2, 128, latent_hw, 4, frames_k, tile, 0.3, "scaled_dot_product", qk_fp8=True)
+    print(f"[gpu] fp8 fused vs tiled {latent_hw} tile={tile} text={text} {layout}", flush=True)
+    q, k, v = make_qkv(wl, seed=11, layout=layout)
+    g = torch.Generator().manual_seed(12)
+    kt = torch.randn(1, 2, text, 128, generator=g).to(torch.bfloat16).to(dev) if text else None
+    vt = torch.randn(1, 2, text, 128, generator=g).to(torch.bfloat16).to(dev) if text else None
+    params = dict(wl.sparse_params(), tile_size=tile)
+
+    def select(q_pool, k_pool, tl, grid_q, grid_k):
+        return fast_generate_indices(q_pool, k_pool, tl, grid_q, grid_k, params, dev)
+
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    assert _pipeline.uses_fused(qd, kd, vd, tile, latent_hw)
+    out_f = _pipeline.sparse_attention(qd, kt, vt, kd, vd, latent_hw, tile, select, qk_fp8=True, fused=True)
+    out_t = _pipeline.sparse_attention(qd, kt, vt, kd, vd, latent_hw, tile, select, qk_fp8=True, fused=False)
+    torch.cuda.synchronize()
+    assert out_f.stride() == qd.stride()
+    assert torch.equal(out_f.view(torch.int16), out_t.view(torch.int16))
