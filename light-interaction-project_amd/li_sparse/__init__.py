@@ -11,7 +11,12 @@ Drop-in modules with the reference's call signatures:
 * ``li_sparse.mg.bi_sparse_operation``: ``run_sparse_attention``, ``generate_prefill_indices``
   (matrix-game-3.0/files/wan/modules/bi_sparse_operation.py)
 
+``ContextCache`` keeps the key-side preparation of the fixed context frames
+and the text across the denoise steps of a chunk (``sparse_params`` keys
+``context_cache`` and ``context_frames``).
+
 All compute runs in the HIP kernels of ``libli_sparse_attn.so``; importing this
 package fails if the library is not built.
 """
 from . import _lib  # noqa: F401  (fails loudly when the native library is missing)
+from ._pipeline import ContextCache  # noqa: F401

@@ -83,30 +83,123 @@ def qk_fp8(sparse_params):
     return bool(sparse_params.get("qk_fp8", False))
 
 
-def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance):
+class ContextCache:
+    """Prepared key-side blocks of the fixed context of K/V, kept across calls.
+
+    HY-WorldPlay recomputes the current chunk's K/V at every denoise step while
+    the memory frames' K/V and the text stay fixed for the chunk; the reference
+    re-tiles all of it on every call (ar_sparse_operation.py:337-348).  Pass a
+    cache as ``sparse_params["context_cache"]`` with
+    ``sparse_params["context_frames"]``, the number of leading K frames that do
+    not change until the next ``reset()``.  The first call per layer
+    (``block_idx``) and shape prepares every key block (pools; e4m3 codes and
+    scales; tiles on the tiled paths) and keeps the buffers; later calls
+    prepare only the blocks from the first t-slab that is not entirely
+    context (the context is rounded down to whole ``tt``-frame slabs) and the
+    text blocks not at all.  Results are bit-identical to uncached calls.  Call
+    ``reset()`` whenever the context or the text changes (a new chunk);
+    calls that share a cache must run on one stream.
+    """
+
+    def __init__(self):
+        self._entries = {}
+
+    def reset(self):
+        self._entries.clear()
+
+    def __len__(self):
+        return len(self._entries)
+
+
+def context_of(sparse_params, block_idx):
+    """(cache, layer, frames) from ``sparse_params`` for ``sparse_attention``, or None without a cache."""
+    cache = sparse_params.get("context_cache")
+    if cache is None:
+        return None
+    if not isinstance(cache, ContextCache):
+        raise TypeError("sparse_params['context_cache'] must be a li_sparse.ContextCache")
+    return cache, block_idx, int(sparse_params.get("context_frames", 0))
+
+
+def _pad_text(x, g, text_len):
+    pad = g.num_txt_blk * g.bs - text_len
+    return (F.pad(x, (0, 0, 0, pad)) if pad > 0 else x).contiguous()
+
+
+def _k_side(path, k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, dt):
+    """Key-side buffers of one call: text blocks, then the visual blocks from the first uncached frame.
+
+    path: "fused" (K pool; padded text K/V), "fused_fp8" (e4m3 K tiles + scales, K pool; padded text V),
+    "tiled" (K/V tiles, K pool), "tiled_fp8" (e4m3 K tiles + scales, V tiles, K pool).
+    """
+    cache, layer, cframes = ctx if ctx is not None else (None, None, 0)
+    cf = min((max(cframes, 0) // g.tt) * g.tt, g.T_k) if cache is not None else 0
+    key = (path, layer, B, NH, D, dt, str(dev), g, text_len, cf)
+    bufs = cache._entries.get(key) if cache is not None else None
+    first = cf if bufs is not None else 0
+    nkb = g.num_txt_blk + g.nk_blk
+    if bufs is None:
+        bufs = {"k_pool": torch.empty((B, NH, g.nk_blk, D), device=dev, dtype=dt)}
+        if path in ("fused_fp8", "tiled_fp8"):
+            bufs["k8"] = torch.empty((B, NH, nkb, g.bs, D), device=dev, dtype=_core.FP8)
+            bufs["k_scale"] = torch.empty((B, NH, nkb), device=dev, dtype=torch.float32)
+        if path == "tiled":
+            bufs["k_all"] = torch.empty((B, NH, nkb, g.bs, D), device=dev, dtype=dt)
+        if path in ("tiled", "tiled_fp8"):
+            bufs["v_all"] = torch.empty((B, NH, nkb, g.bs, D), device=dev, dtype=dt)
+        bufs["kt"] = bufs["vt"] = None
+        if text_len > 0:
+            kt, vt = _pad_text(k_txt, g, text_len), _pad_text(v_txt, g, text_len)
+            if path == "fused":
+                bufs["kt"], bufs["vt"] = kt, vt
+            elif path == "fused_fp8":
+                bufs["vt"] = vt
+            if path in ("fused_fp8", "tiled_fp8"):
+                # Contiguous text blocks: the trivial grid T = blocks, H = 1, W = BS, tile (1, 1, BS).
+                _core.tile_prep_fp8(kt, bufs["k8"], bufs["k_scale"], None, 0, 0, g.num_txt_blk, 1, g.bs, 1, 1, g.bs,
+                                    1, 1)
+            if path == "tiled":
+                bufs["k_all"][:, :, :g.num_txt_blk].copy_(kt.view(B, NH, g.num_txt_blk, g.bs, D))
+            if path in ("tiled", "tiled_fp8"):
+                bufs["v_all"][:, :, :g.num_txt_blk].copy_(vt.view(B, NH, g.num_txt_blk, g.bs, D))
+        if cache is not None:
+            cache._entries[key] = bufs
+    T = g.T_k - first
+    if T > 0:
+        fb = (first // g.tt) * g.nh * g.nw
+        tok = first * g.H * g.W
+        kv, vv = k_vis[:, :, tok:], v_vis[:, :, tok:]
+        geo = (T, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+        if path == "fused":
+            _core.pool(kv, bufs["k_pool"], fb, *geo)
+        elif path == "fused_fp8":
+            _core.tile_prep_fp8(kv, bufs["k8"], bufs["k_scale"], bufs["k_pool"], g.num_txt_blk + fb, fb, *geo)
+        elif path == "tiled":
+            _core.kv_prep(kv, vv, bufs["k_all"], bufs["v_all"], bufs["k_pool"], g.num_txt_blk + fb, fb, *geo)
+        else:
+            _core.kv_prep_fp8(kv, vv, bufs["k8"], bufs["k_scale"], bufs["v_all"], bufs["k_pool"], g.num_txt_blk + fb,
+                              fb, *geo)
+    return bufs
+
+
+def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance, ctx):
     """Pools, block selection, then one kernel that gathers, attends and untiles."""
     B, NH, _, D = q.shape
     dev, dt = q.device, q.dtype
     _stage(events, "alloc_start")
     q_pool = torch.empty((B, NH, g.nq_blk, D), device=dev, dtype=dt)
-    k_pool = torch.empty((B, NH, g.nk_blk, D), device=dev, dtype=dt)
-    kt = vt = None
-    if text_len > 0:
-        pad = g.num_txt_blk * g.bs - text_len
-        kt = (F.pad(k_txt, (0, 0, 0, pad)) if pad > 0 else k_txt).contiguous()
-        vt = (F.pad(v_txt, (0, 0, 0, pad)) if pad > 0 else v_txt).contiguous()
     o_out = torch.empty_like(q)
     _stage(events, "alloc_end")
     _stage(events, "prep_start")
     _core.pool(q, q_pool, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
-    _core.pool(k_vis, k_pool, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    kb = _k_side("fused", k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, dt)
     _stage(events, "prep_end")
     _stage(events, "index_start")
-    indices, counts = select(q_pool, k_pool, text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
+    indices, counts = select(q_pool, kb["k_pool"], text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
     _stage(events, "index_end")
     _stage(events, "attn_start")
-    _core.bsa_forward_gather(q, k_vis, v_vis, kt, vt, g.num_txt_blk, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw,
-                             g.nh, g.nw, indices, counts, 1.0 / math.sqrt(D), o_out, balance=balance)
+    _core.bsa_forward_gather(q, k_vis, v_vis, kb["kt"], kb["vt"], g.num_txt_blk, g.T_q, g.T_k, g.H, g.W, g.tt, g.th,
+                             g.tw, g.nh, g.nw, indices, counts, 1.0 / math.sqrt(D), o_out, balance=balance)
     _stage(events, "attn_end")
     _stage(events, "untile_start")
     _stage(events, "untile_end")
@@ -118,43 +211,34 @@ def fp8_supported(D, tile):
     return D == 128 and tile[0] * tile[1] * tile[2] == 128
 
 
-def _tiled_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance):
+def _q_fp8(q, g, B, NH, D, dev):
+    q8 = torch.empty((B, NH, g.nq_blk, g.bs, D), device=dev, dtype=_core.FP8)
+    q_scale = torch.empty((B, NH, g.nq_blk), device=dev, dtype=torch.float32)
+    q_pool = torch.empty((B, NH, g.nq_blk, D), device=dev, dtype=q.dtype)
+    _core.tile_prep_fp8(q, q8, q_scale, q_pool, 0, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    return q8, q_scale, q_pool
+
+
+def _tiled_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance, ctx):
     """Tiled sequence with Q and K quantized to e4m3 per tile block (scale amax / 448) in their gathers.
 
     The pools (and so the block selection) are those of the bf16 path; V, P V and the output stay bf16.
     """
     B, NH, _, D = q.shape
     dev = q.device
-    f8 = _core.FP8
     _stage(events, "alloc_start")
-    q8 = torch.empty((B, NH, g.nq_blk, g.bs, D), device=dev, dtype=f8)
-    q_scale = torch.empty((B, NH, g.nq_blk), device=dev, dtype=torch.float32)
-    q_pool = torch.empty((B, NH, g.nq_blk, D), device=dev, dtype=q.dtype)
-    nkb = g.num_txt_blk + g.nk_blk
-    k8 = torch.empty((B, NH, nkb, g.bs, D), device=dev, dtype=f8)
-    k_scale = torch.empty((B, NH, nkb), device=dev, dtype=torch.float32)
-    v_all = torch.empty((B, NH, nkb, g.bs, D), device=dev, dtype=q.dtype)
-    k_pool = torch.empty((B, NH, g.nk_blk, D), device=dev, dtype=q.dtype)
-    if text_len > 0:
-        pad = g.num_txt_blk * g.bs - text_len
-        kt = F.pad(k_txt, (0, 0, 0, pad)) if pad > 0 else k_txt
-        vt = F.pad(v_txt, (0, 0, 0, pad)) if pad > 0 else v_txt
-        v_all[:, :, :g.num_txt_blk].copy_(vt.reshape(B, NH, g.num_txt_blk, g.bs, D))
     _stage(events, "alloc_end")
     _stage(events, "prep_start")
-    if text_len > 0:
-        # Contiguous text blocks: the trivial grid T = blocks, H = 1, W = BS, tile (1, 1, BS).
-        _core.tile_prep_fp8(kt, k8, k_scale, None, 0, 0, g.num_txt_blk, 1, g.bs, 1, 1, g.bs, 1, 1)
-    _core.tile_prep_fp8(q, q8, q_scale, q_pool, 0, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
-    _core.kv_prep_fp8(k_vis, v_vis, k8, k_scale, v_all, k_pool, g.num_txt_blk, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw,
-                      g.nh, g.nw)
+    q8, q_scale, q_pool = _q_fp8(q, g, B, NH, D, dev)
+    kb = _k_side("tiled_fp8", k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, q.dtype)
     _stage(events, "prep_end")
     _stage(events, "index_start")
-    indices, counts = select(q_pool, k_pool, text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
+    indices, counts = select(q_pool, kb["k_pool"], text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
     _stage(events, "index_end")
     _stage(events, "attn_start")
-    o_flat = _core.bsa_forward_fp8(q8.flatten(2, 3), q_scale, k8.flatten(2, 3), k_scale, v_all.flatten(2, 3),
-                                   indices, counts, 1.0 / math.sqrt(D), g.bs, balance=balance)
+    o_flat = _core.bsa_forward_fp8(q8.flatten(2, 3), q_scale, kb["k8"].flatten(2, 3), kb["k_scale"],
+                                   kb["v_all"].flatten(2, 3), indices, counts, 1.0 / math.sqrt(D), g.bs,
+                                   balance=balance)
     _stage(events, "attn_end")
     _stage(events, "untile_start")
     o_out = torch.empty_like(q)
@@ -163,38 +247,23 @@ def _tiled_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, ev
     return o_out if o_out.dtype == out_dtype else o_out.to(out_dtype)
 
 
-def _fused_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance):
+def _fused_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance, ctx):
     """e4m3 Q/K tiles from the quantizing gathers, then one kernel that reads V and writes O in token order."""
     B, NH, _, D = q.shape
     dev = q.device
-    f8 = _core.FP8
     _stage(events, "alloc_start")
-    q8 = torch.empty((B, NH, g.nq_blk, g.bs, D), device=dev, dtype=f8)
-    q_scale = torch.empty((B, NH, g.nq_blk), device=dev, dtype=torch.float32)
-    q_pool = torch.empty((B, NH, g.nq_blk, D), device=dev, dtype=q.dtype)
-    nkb = g.num_txt_blk + g.nk_blk
-    k8 = torch.empty((B, NH, nkb, g.bs, D), device=dev, dtype=f8)
-    k_scale = torch.empty((B, NH, nkb), device=dev, dtype=torch.float32)
-    k_pool = torch.empty((B, NH, g.nk_blk, D), device=dev, dtype=q.dtype)
-    vt = None
-    if text_len > 0:
-        pad = g.num_txt_blk * g.bs - text_len
-        kt = F.pad(k_txt, (0, 0, 0, pad)) if pad > 0 else k_txt
-        vt = (F.pad(v_txt, (0, 0, 0, pad)) if pad > 0 else v_txt).contiguous()
     o_out = torch.empty_like(q)
     _stage(events, "alloc_end")
     _stage(events, "prep_start")
-    if text_len > 0:
-        _core.tile_prep_fp8(kt, k8, k_scale, None, 0, 0, g.num_txt_blk, 1, g.bs, 1, 1, g.bs, 1, 1)
-    _core.tile_prep_fp8(q, q8, q_scale, q_pool, 0, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
-    _core.tile_prep_fp8(k_vis, k8, k_scale, k_pool, g.num_txt_blk, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    q8, q_scale, q_pool = _q_fp8(q, g, B, NH, D, dev)
+    kb = _k_side("fused_fp8", k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, q.dtype)
     _stage(events, "prep_end")
     _stage(events, "index_start")
-    indices, counts = select(q_pool, k_pool, text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
+    indices, counts = select(q_pool, kb["k_pool"], text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
     _stage(events, "index_end")
     _stage(events, "attn_start")
-    _core.bsa_forward_fp8_gather(q8.flatten(2, 3), q_scale, k8.flatten(2, 3), k_scale, v_vis, vt, g.num_txt_blk,
-                                 g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw, indices, counts,
+    _core.bsa_forward_fp8_gather(q8.flatten(2, 3), q_scale, kb["k8"].flatten(2, 3), kb["k_scale"], v_vis, kb["vt"],
+                                 g.num_txt_blk, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw, indices, counts,
                                  1.0 / math.sqrt(D), o_out, balance=balance)
     _stage(events, "attn_end")
     _stage(events, "untile_start")
@@ -203,7 +272,7 @@ def _fused_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, ev
 
 
 def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, events=None, fused=True,
-                     balance=False, qk_fp8=False):
+                     balance=False, qk_fp8=False, context=None):
     """One sparse-attention forward.
 
     q (B,H,Lq,D); k_txt/v_txt (B,H,N_txt,D) or None; k_vis/v_vis (B,H,Lk,D), any strides.
@@ -216,6 +285,8 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
     attention / untile.  Both give the same bits.  ``balance`` (rows with their own budgets) starts
     the longest query tiles first.  ``qk_fp8`` takes Q K^T on e4m3 codes with one scale per tile
     block (bf16 only; D = 128 and 128-token tiles, ValueError otherwise); the selection is unchanged.
+    ``context`` = (ContextCache, layer key, context frames) keeps the key-side preparation of the
+    fixed leading frames and the text across calls (see ContextCache).
     """
     out_dtype = q.dtype
     if q.dtype not in (torch.bfloat16, torch.float16):
@@ -226,39 +297,30 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
     g = geometry(latent_hw, tile, q.shape[2], k_vis.shape[2], text_len)
     B, NH, _, D = q.shape
     dev, dt = q.device, q.dtype
+    args = (q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance, context)
     if qk_fp8:
         if dt != torch.bfloat16 or not fp8_supported(D, tile):
             raise ValueError(f"qk_fp8 is built for bfloat16, D = 128 and 128-token tiles (got {dt}, D = {D}, "
                              f"tile {tuple(tile)})")
         if fused and uses_fused(q, k_vis, v_vis, tile, (g.H, g.W)):
-            return _fused_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance)
-        return _tiled_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance)
+            return _fused_fp8(*args)
+        return _tiled_fp8(*args)
     if fused and uses_fused(q, k_vis, v_vis, tile, (g.H, g.W)):
-        return _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance)
+        return _fused(*args)
     _stage(events, "alloc_start")
     q_tiled = torch.empty((B, NH, g.nq_blk, g.bs, D), device=dev, dtype=dt)
     q_pool = torch.empty((B, NH, g.nq_blk, D), device=dev, dtype=dt)
-    k_all = torch.empty((B, NH, g.num_txt_blk + g.nk_blk, g.bs, D), device=dev, dtype=dt)
-    v_all = torch.empty((B, NH, g.num_txt_blk + g.nk_blk, g.bs, D), device=dev, dtype=dt)
-    k_pool = torch.empty((B, NH, g.nk_blk, D), device=dev, dtype=dt)
-    if text_len > 0:
-        pad = g.num_txt_blk * g.bs - text_len
-        kt = F.pad(k_txt, (0, 0, 0, pad)) if pad > 0 else k_txt
-        vt = F.pad(v_txt, (0, 0, 0, pad)) if pad > 0 else v_txt
-        k_all[:, :, :g.num_txt_blk].copy_(kt.reshape(B, NH, g.num_txt_blk, g.bs, D))
-        v_all[:, :, :g.num_txt_blk].copy_(vt.reshape(B, NH, g.num_txt_blk, g.bs, D))
     _stage(events, "alloc_end")
     _stage(events, "prep_start")
     _core.q_prep(q, q_tiled, q_pool, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
-    _core.kv_prep(k_vis, v_vis, k_all, v_all, k_pool, g.num_txt_blk, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw,
-                  g.nh, g.nw)
+    kb = _k_side("tiled", k_txt, v_txt, k_vis, v_vis, g, text_len, context, B, NH, D, dev, dt)
     _stage(events, "prep_end")
     _stage(events, "index_start")
-    indices, counts = select(q_pool, k_pool, text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
+    indices, counts = select(q_pool, kb["k_pool"], text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
     _stage(events, "index_end")
     _stage(events, "attn_start")
-    o_flat = _core.bsa_forward(q_tiled.flatten(2, 3), k_all.flatten(2, 3), v_all.flatten(2, 3), indices, counts,
-                               1.0 / math.sqrt(D), g.bs, balance=balance)
+    o_flat = _core.bsa_forward(q_tiled.flatten(2, 3), kb["k_all"].flatten(2, 3), kb["v_all"].flatten(2, 3), indices,
+                               counts, 1.0 / math.sqrt(D), g.bs, balance=balance)
     _stage(events, "attn_end")
     _stage(events, "untile_start")
     o_out = torch.empty_like(q)
