@@ -18,14 +18,17 @@
 //    of a double product) and the remaining k - n_forced blocks are the
 //    largest non-forced scores, ties to the lower index: every key block gets
 //    the unique 32-bit key (order-preserving score bits << 16 | 0xFFFF - j;
-//    0 marks a forced block) and a 32-step bitwise search finds the exact
-//    (k - n_forced)-th largest key;
+//    0 marks a forced block) and a bitwise search of at most 32 steps finds
+//    the exact (k - n_forced)-th largest key;
 // 4. the selected blocks are written in ascending order by a ballot/prefix
 //    compaction over j, which replaces the reference's topk + sort.
 //
-// One wave per query row, WAVES rows per workgroup: every reduction is a
-// ballot + popcount inside the wave, so the kernel has no workgroup barrier.
-// The wave's keys live in its own LDS slice (4 bytes per key block).
+// One wave per query row: every per-row reduction is a ballot + popcount
+// inside the wave, and the row's 32-bit keys live in LDS (4 bytes per key
+// block).  Aligned pools with a unit d stride take the shared-pool kernel (4
+// rows of one head per workgroup, the head's pool streamed once through LDS
+// tiles); other pools and very long key grids take the generic kernel, in which
+// each wave reads the pool rows itself.
 #include "li_common.hpp"
 
 namespace li {
@@ -81,159 +84,14 @@ __device__ __forceinline__ float norm_den(const float* x) {
 
 __device__ __forceinline__ int wave_count(bool pred) { return __popcll(__ballot(pred)); }
 
-#define LI_MASK_INLINE __attribute__((always_inline))
-
-// KR > 0: nk <= 64 KR and contiguous pool rows; a lane keeps the keys of
-// blocks lane, lane + 64, ... in registers and computes their dot products
-// side by side (each still summed over d in order).  KR = 0: any nk, keys
-// in the wave's LDS slice.
-template <typename E, int D, int KR>
-__global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a, int waves) {
-  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
+// Steps 3 and 4 for query row qb of (b, h) = bh, run by one wave: key_at(r)
+// is the key of block 64 r + lane (0 for forced blocks and past nk), nchunk =
+// ceil(nk / 64), nf the number of forced blocks.
+template <int KUNROLL, typename KeyAt>
+__device__ __forceinline__ void select_row(const MaskArgs& a, KeyAt&& key_at, int nchunk, int nf, int qb, int bh,
+                                           int lane) {
   const li_mask_params& p = a.p;
   const int nk = p.nk;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int qb = blockIdx.x * waves + wave;
-  const int bh = blockIdx.y;
-  if (qb >= p.nq) return;  // whole wave leaves; no workgroup barrier follows
-  const int b = bh / a.NH, h = bh % a.NH;
-  const bool cosine = p.metric == LI_METRIC_COSINE;
-  uint32_t* keys = smem + (size_t)wave * (nk + D);
-  float* qv = reinterpret_cast<float*>(keys + nk);
-
-  // 1a. query pool row, normalised for cosine (every lane computes the same
-  // sequential normaliser; lanes then own elements lane, lane + 64, ...).
-  const uint16_t* qrow = a.qp + b * a.qs[0] + h * a.qs[1] + (int64_t)qb * a.qs[2];
-  for (int d = lane; d < D; d += 64) qv[d] = E::to_f32(qrow[(int64_t)d * a.qs[3]]);
-  __builtin_amdgcn_wave_barrier();
-  if (cosine) {
-    float ss = 0.0f;
-    for (int d = 0; d < D; ++d) ss = ss + qv[d] * qv[d];
-    const float nrm = E::to_f32(E::from_f32(__builtin_sqrtf(ss)));
-    const float eps = E::to_f32(E::from_f32(1e-12f));
-    const float den = nrm > eps ? nrm : eps;
-    __builtin_amdgcn_wave_barrier();
-    for (int d = lane; d < D; d += 64) qv[d] = E::to_f32(E::from_f32(qv[d] / den));
-    __builtin_amdgcn_wave_barrier();
-  }
-
-  // 1b/2. scores, forced flags, order keys.
-  const int pos = nk - p.nq + qb;  // query block's position in the key grid
-  const int hw = p.nh * p.nw;
-  const int pt = pos / hw, ph = (pos % hw) / p.nw, pw = pos % p.nw;
-  const bool vec = a.ks[3] == 1 && (reinterpret_cast<uintptr_t>(a.kp) & 15u) == 0 && a.ks[0] % 8 == 0 &&
-                   a.ks[1] % 8 == 0 && a.ks[2] % 8 == 0;
-  const uint16_t* kbase = a.kp + b * a.ks[0] + h * a.ks[1];
-  uint16_t* srow = a.scores ? a.scores + ((int64_t)bh * p.nq + qb) * nk : nullptr;
-  // Score bits of block j -> forced flag and order key.
-  auto finish = [&](int j, float dot, bool& f) {
-    uint16_t s = E::from_f32(dot);
-    if (p.metric == LI_METRIC_SCALED_DOT) s = E::from_f32(E::to_f32(s) * p.scale);
-    if (srow) srow[j] = s;
-    f = (p.n_recent > 0) && (j >= nk - p.n_recent);
-    if (p.force_diag && j == pos) f = true;
-    if (p.force_sink && j == qb % hw) f = true;
-    if (p.force_neighbors && pos >= 0 && pos < nk) {
-      const int jt = j / hw, jh = (j % hw) / p.nw, jw = j % p.nw;
-      if (abs(jt - pt) + abs(jh - ph) + abs(jw - pw) <= 1) f = true;
-    }
-    return f ? 0u : ((order16(s) << 16) | (0xFFFFu - (uint32_t)j));
-  };
-  int nf = 0;
-  uint32_t kr[KR > 0 ? KR : 1];
-  if constexpr (KR > 0) {
-    // Dot products of this lane's KR blocks, 8 dimensions at a time.
-    float dot[KR], den[KR];
-#pragma unroll
-    for (int r = 0; r < KR; ++r) {
-      dot[r] = 0.0f;
-      den[r] = 1.0f;
-    }
-    if (cosine) {
-      float ss[KR];
-#pragma unroll
-      for (int r = 0; r < KR; ++r) ss[r] = 0.0f;
-#pragma unroll
-      for (int c = 0; c < D / 8; ++c)
-#pragma unroll
-        for (int r = 0; r < KR; ++r) {
-          const int j = r * 64 + lane;
-          if (j < nk) {
-            const u32x4 w = *reinterpret_cast<const u32x4*>(kbase + (int64_t)j * a.ks[2] + 8 * c);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              const float x = E::to_f32(uint16_t((w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu));
-              ss[r] = ss[r] + x * x;
-            }
-          }
-        }
-      const float eps = E::to_f32(E::from_f32(1e-12f));
-#pragma unroll
-      for (int r = 0; r < KR; ++r) {
-        const float nrm = E::to_f32(E::from_f32(__builtin_sqrtf(ss[r])));
-        den[r] = nrm > eps ? nrm : eps;
-      }
-    }
-#pragma unroll
-    for (int c = 0; c < D / 8; ++c) {
-      float q8[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) q8[i] = qv[8 * c + i];
-#pragma unroll
-      for (int r = 0; r < KR; ++r) {
-        const int j = r * 64 + lane;
-        if (j < nk) {
-          const u32x4 w = *reinterpret_cast<const u32x4*>(kbase + (int64_t)j * a.ks[2] + 8 * c);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            float x = E::to_f32(uint16_t((w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu));
-            if (cosine) x = E::to_f32(E::from_f32(x / den[r]));
-            dot[r] = dot[r] + q8[i] * x;
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < KR; ++r) {
-      const int j = r * 64 + lane;
-      bool f = false;
-      kr[r] = 0u;
-      if (j < nk) kr[r] = finish(j, dot[r], f);
-      nf += wave_count(f);
-    }
-  } else {
-    for (int j0 = 0; j0 < nk; j0 += 64) {
-      const int j = j0 + lane;
-      bool f = false;
-      if (j < nk) {
-        float x[D];
-        load_row<E, D>(kbase + (int64_t)j * a.ks[2], a.ks[3], vec, x);
-        float dot = 0.0f;
-        if (cosine) {
-          const float den = norm_den<E, D>(x);
-#pragma unroll
-          for (int d = 0; d < D; ++d) dot = dot + qv[d] * E::to_f32(E::from_f32(x[d] / den));
-        } else {
-#pragma unroll
-          for (int d = 0; d < D; ++d) dot = dot + qv[d] * x[d];
-        }
-        keys[j] = finish(j, dot, f);
-      }
-      nf += wave_count(f);
-    }
-  }
-  __builtin_amdgcn_wave_barrier();
-  // Key of block r * 64 + lane (0 past nk: never selected, never counted).
-  auto key_at = [&](int r) LI_MASK_INLINE {
-    if constexpr (KR > 0) {
-      return kr[r];
-    } else {
-      const int j = r * 64 + lane;
-      return j < nk ? keys[j] : 0u;
-    }
-  };
-  const int nchunk = KR > 0 ? KR : (nk + 63) / 64;
-  constexpr int KUNROLL = KR > 0 ? KR : 1;
 
   // 3. budget.
   int k;
@@ -253,20 +111,35 @@ __global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a, int waves) 
     k = k > nk ? nk : k;
     k = k < nf ? nf : k;
   }
-  const int kk = k - nf;  // non-forced blocks to keep
+  // Wave-uniform, so the search below runs on scalar registers.
+  const int kk = __builtin_amdgcn_readfirstlane(k - nf);  // non-forced blocks to keep
   const int nfree = nk - nf;
 
-  // Exact kk-th largest key among non-forced blocks (forced keys are 0 and
-  // never reach a candidate, which is always >= 1 here).
+  // Threshold thr with exactly kk non-forced keys >= thr: the kk-th largest
+  // key, found bit by bit from the top (forced keys are 0 and never reach a
+  // candidate, which is always >= 1 here).  The search stops as soon as a
+  // candidate has exactly kk keys at or above it -- the same set as the
+  // kk-th largest key selects -- which for distinct scores happens within the
+  // 16 score bits.
+  // Index bits 15 .. L-1 of the low half are 1 in every key (0xFFFF - j with
+  // j < nk <= 2^L), so those steps keep their bit without counting.
   uint32_t thr = 1u;
   if (kk > 0 && kk < nfree) {
+    const int L = nk > 1 ? 32 - __builtin_clz((uint32_t)(nk - 1)) : 0;
     uint32_t prefix = 0;
     for (int bit = 31; bit >= 0; --bit) {
+      if (bit < 16 && bit >= L) {
+        prefix |= 1u << bit;
+        continue;
+      }
       const uint32_t cand = prefix | (1u << bit);
       int c = 0;
 #pragma unroll KUNROLL
       for (int r = 0; r < nchunk; ++r) c += wave_count(key_at(r) >= cand);
-      if (c >= kk) prefix = cand;
+      if (c >= kk) {
+        prefix = cand;
+        if (c == kk) break;
+      }
     }
     thr = prefix;
   }
@@ -292,6 +165,258 @@ __global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a, int waves) 
   }
   for (int i = ntxt + k + lane; i < p.kmax; i += 64) irow[i] = 0;
   if (lane == 0) a.counts[row] = ntxt + k;
+}
+
+#define LI_MASK_INLINE __attribute__((always_inline))
+
+// Query row qb of (b, h) into qv (fp32, D values), normalised for cosine: every
+// lane computes the same sequential normaliser; lanes own d = lane, lane + 64, ...
+template <typename E, int D>
+__device__ __forceinline__ void load_query(const MaskArgs& a, int b, int h, int qb, bool cosine, float* qv,
+                                           int lane) {
+  const uint16_t* qrow = a.qp + b * a.qs[0] + h * a.qs[1] + (int64_t)qb * a.qs[2];
+  for (int d = lane; d < D; d += 64) qv[d] = E::to_f32(qrow[(int64_t)d * a.qs[3]]);
+  __builtin_amdgcn_wave_barrier();
+  if (cosine) {
+    float ss = 0.0f;
+    for (int d = 0; d < D; ++d) ss = ss + qv[d] * qv[d];
+    const float nrm = E::to_f32(E::from_f32(__builtin_sqrtf(ss)));
+    const float eps = E::to_f32(E::from_f32(1e-12f));
+    const float den = nrm > eps ? nrm : eps;
+    __builtin_amdgcn_wave_barrier();
+    for (int d = lane; d < D; d += 64) qv[d] = E::to_f32(E::from_f32(qv[d] / den));
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+// Step 1b/2 for one (row, block): score bits from the fp32 dot product, the
+// forced flag, and the order key (0 for a forced block).
+struct RowGeom {
+  int nk, qb, pos, hw, pt, ph, pw;
+  __device__ RowGeom(const li_mask_params& p, int qb_) : nk(p.nk), qb(qb_) {
+    pos = p.nk - p.nq + qb;  // query block's position in the key grid
+    hw = p.nh * p.nw;
+    pt = pos / hw;
+    ph = (pos % hw) / p.nw;
+    pw = pos % p.nw;
+  }
+};
+
+template <typename E>
+__device__ __forceinline__ uint32_t finish_key(const li_mask_params& p, const RowGeom& g, uint16_t* srow, int j,
+                                               float dot, bool& f) {
+  uint16_t s = E::from_f32(dot);
+  if (p.metric == LI_METRIC_SCALED_DOT) s = E::from_f32(E::to_f32(s) * p.scale);
+  if (srow) srow[j] = s;
+  f = (p.n_recent > 0) && (j >= g.nk - p.n_recent);
+  if (p.force_diag && j == g.pos) f = true;
+  if (p.force_sink && j == g.qb % g.hw) f = true;
+  if (p.force_neighbors && g.pos >= 0 && g.pos < g.nk) {
+    const int jt = j / g.hw, jh = (j % g.hw) / p.nw, jw = j % p.nw;
+    if (abs(jt - g.pt) + abs(jh - g.ph) + abs(jw - g.pw) <= 1) f = true;
+  }
+  return f ? 0u : ((order16(s) << 16) | (0xFFFFu - (uint32_t)j));
+}
+
+// Generic path (any pool strides, any nk <= kMaxNk): one wave per query row,
+// `waves` rows per workgroup, each wave reading its head's pool rows itself;
+// the keys live in the wave's LDS slice (nk + D words).
+template <typename E, int D>
+__global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a, int waves) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
+  const li_mask_params& p = a.p;
+  const int nk = p.nk;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int qb = blockIdx.x * waves + wave;
+  const int bh = blockIdx.y;
+  if (qb >= p.nq) return;  // whole wave leaves; no workgroup barrier follows
+  const int b = bh / a.NH, h = bh % a.NH;
+  const bool cosine = p.metric == LI_METRIC_COSINE;
+  uint32_t* keys = smem + (size_t)wave * (nk + D);
+  float* qv = reinterpret_cast<float*>(keys + nk);
+  load_query<E, D>(a, b, h, qb, cosine, qv, lane);
+
+  const RowGeom g(p, qb);
+  const bool vec = a.ks[3] == 1 && (reinterpret_cast<uintptr_t>(a.kp) & 15u) == 0 && a.ks[0] % 8 == 0 &&
+                   a.ks[1] % 8 == 0 && a.ks[2] % 8 == 0;
+  const uint16_t* kbase = a.kp + b * a.ks[0] + h * a.ks[1];
+  uint16_t* srow = a.scores ? a.scores + ((int64_t)bh * p.nq + qb) * nk : nullptr;
+  int nf = 0;
+  for (int j0 = 0; j0 < nk; j0 += 64) {
+    const int j = j0 + lane;
+    bool f = false;
+    if (j < nk) {
+      float x[D];
+      load_row<E, D>(kbase + (int64_t)j * a.ks[2], a.ks[3], vec, x);
+      float dot = 0.0f;
+      if (cosine) {
+        const float den = norm_den<E, D>(x);
+#pragma unroll
+        for (int d = 0; d < D; ++d) dot = dot + qv[d] * E::to_f32(E::from_f32(x[d] / den));
+      } else {
+#pragma unroll
+        for (int d = 0; d < D; ++d) dot = dot + qv[d] * x[d];
+      }
+      keys[j] = finish_key<E>(p, g, srow, j, dot, f);
+    }
+    nf += wave_count(f);
+  }
+  __builtin_amdgcn_wave_barrier();
+  auto key_at = [&](int r) LI_MASK_INLINE {
+    const int j = r * 64 + lane;
+    return j < nk ? keys[j] : 0u;
+  };
+  select_row<1>(a, key_at, (nk + 63) / 64, nf, qb, bh, lane);
+}
+
+// Shared-pool path (16-byte aligned pools with unit d stride): a workgroup
+// holds 4 query rows of one (b, h), one per wave, and streams the head's pool
+// through LDS in tiles of 64 KT blocks, so each pool row is read from memory
+// once per 4 query rows.  Rows are padded by 16 bytes in LDS so that lanes
+// reading consecutive blocks hit distinct banks.  For cosine, thread t
+// computes the normaliser of block t of the tile and the whole workgroup then
+// divides the tile in place before the dot
+// products.  Per (row, block) the arithmetic is the generic path's: the same
+// sequential fp32 sum over d of the same operands.  The next tile's loads are
+// in flight while the current one is scored, and the selection keeps the
+// row's keys in registers (nk <= 64 KS).
+template <typename E, int D, int KT, int KS>
+__global__ __launch_bounds__(256) void block_mask_tiled_kernel(MaskArgs a) {
+  constexpr int NT = 64 * KT;     // blocks per tile
+  constexpr int RS = 2 * D + 16;  // LDS row stride in bytes
+  constexpr int CH = D / 8;       // 16-byte chunks per pool row
+  constexpr int PF = NT * CH / 256;  // 16-byte chunks per thread per tile
+  static_assert(PF * 256 == NT * CH, "tile must split evenly over the workgroup");
+  extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
+  uint8_t* ktile = reinterpret_cast<uint8_t*>(smem);
+  float* qall = reinterpret_cast<float*>(ktile + NT * RS);
+  float* dn = qall + 4 * D;  // cosine normalisers of the tile's blocks
+  uint32_t* kall = reinterpret_cast<uint32_t*>(dn + NT);
+  const li_mask_params& p = a.p;
+  const int nk = p.nk;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qb = blockIdx.x * 4 + wave;
+  const bool live = qb < p.nq;  // dead waves still take part in the tile loads and barriers
+  const int bh = blockIdx.y, b = bh / a.NH, h = bh % a.NH;
+  const bool cosine = p.metric == LI_METRIC_COSINE;
+  float* qv = qall + wave * D;
+  uint32_t* keys = kall + (size_t)wave * nk;
+  if (live) load_query<E, D>(a, b, h, qb, cosine, qv, lane);
+
+  const RowGeom g(p, qb);
+  const uint16_t* kbase = a.kp + b * a.ks[0] + h * a.ks[1];
+  uint16_t* srow = (a.scores && live) ? a.scores + ((int64_t)bh * p.nq + qb) * nk : nullptr;
+  // Chunk i of this thread: tile row tid / CH + i * (256 / CH), column tid % CH.
+  const int r0 = tid / CH, cc = tid % CH;
+  u32x4 pf[PF];
+  auto fetch = [&](int j0) LI_MASK_INLINE {
+    const int nt = nk - j0 < NT ? nk - j0 : NT;
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int r = r0 + i * (256 / CH);
+      if (r < nt) pf[i] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)(j0 + r) * a.ks[2] + 8 * cc);
+    }
+  };
+  // The query row in registers for the dot products (wave-uniform values;
+  // stale on dead waves, never used there).
+  float qr[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) qr[d] = qv[d];
+  int nf = 0;
+  fetch(0);
+  for (int j0 = 0; j0 < nk; j0 += NT) {
+    const int nt = nk - j0 < NT ? nk - j0 : NT;
+    __syncthreads();  // the previous tile is consumed
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int r = r0 + i * (256 / CH);
+      if (r < nt) *reinterpret_cast<u32x4*>(ktile + r * RS + 16 * cc) = pf[i];
+    }
+    __syncthreads();
+    if (j0 + NT < nk) fetch(j0 + NT);
+    if (cosine) {
+      if (tid < nt) {
+        uint8_t* row = ktile + tid * RS;
+        float ss = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+          const u32x4 w = *reinterpret_cast<const u32x4*>(row + 16 * c);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float x = E::to_f32(uint16_t((w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu));
+            ss = ss + x * x;
+          }
+        }
+        const float nrm = E::to_f32(E::from_f32(__builtin_sqrtf(ss)));
+        const float eps = E::to_f32(E::from_f32(1e-12f));
+        dn[tid] = nrm > eps ? nrm : eps;
+      }
+      __syncthreads();
+      // The divisions, spread over the whole workgroup: each thread rewrites
+      // the chunks it stored.
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        const int r = r0 + i * (256 / CH);
+        if (r < nt) {
+          u32x4* at = reinterpret_cast<u32x4*>(ktile + r * RS + 16 * cc);
+          u32x4 w = *at;
+          const float den = dn[r];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t lo = E::from_f32(E::to_f32(uint16_t(w[e] & 0xFFFFu)) / den);
+            const uint32_t hi = E::from_f32(E::to_f32(uint16_t(w[e] >> 16)) / den);
+            w[e] = lo | (hi << 16);
+          }
+          *at = w;
+        }
+      }
+      __syncthreads();
+    }
+    if (live) {
+      // Rows past nt hold stale data; their sums are computed and dropped, so
+      // the LDS reads carry no branch and can be issued ahead.
+      float dot[KT];
+#pragma unroll
+      for (int i = 0; i < KT; ++i) dot[i] = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+#pragma unroll
+        for (int i = 0; i < KT; ++i) {
+          const u32x4 w = *reinterpret_cast<const u32x4*>(ktile + (lane + 64 * i) * RS + 16 * c);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            dot[i] = dot[i] + qr[8 * c + e] * E::to_f32(uint16_t((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < KT; ++i) {
+        const int jl = lane + 64 * i;
+        bool f = false;
+        if (jl < nt) keys[j0 + jl] = finish_key<E>(p, g, srow, j0 + jl, dot[i], f);
+        nf += wave_count(f);
+      }
+    }
+  }
+  if (!live) return;
+  __builtin_amdgcn_wave_barrier();
+  uint32_t kr[KS];
+#pragma unroll
+  for (int r = 0; r < KS; ++r) {
+    const int j = r * 64 + lane;
+    kr[r] = j < nk ? keys[j] : 0u;
+  }
+  select_row<KS>(a, [&](int r) LI_MASK_INLINE { return kr[r]; }, KS, nf, qb, bh, lane);
+}
+
+constexpr int kTiledKt = 2;
+constexpr int kTiledMaxNk = 64 * 28;
+
+// LDS bytes of the shared-pool path, or 0 when it does not apply.
+size_t tiled_lds(int D, int nk, bool vec_k) {
+  if (!vec_k || nk > kTiledMaxNk) return 0;
+  const size_t bytes =
+      (size_t)64 * kTiledKt * (2 * D + 16 + 4) + (size_t)4 * D * 4 + (size_t)4 * nk * 4;
+  return bytes <= 65536 ? bytes : 0;
 }
 
 }  // namespace
@@ -328,27 +453,30 @@ extern "C" int li_block_mask(int dtype, int32_t B, int32_t NH, int32_t D, const 
   a.counts = counts;
   a.scores = static_cast<uint16_t*>(scores);
   a.NH = NH;
-  // Per-wave LDS slice: nk keys (LDS path only) + the query row; up to 4
-  // waves (rows) per workgroup.
   const bool vec_k = k_pool_strides[3] == 1 && (reinterpret_cast<uintptr_t>(k_pool) & 15u) == 0 &&
                      k_pool_strides[0] % 8 == 0 && k_pool_strides[1] % 8 == 0 && k_pool_strides[2] % 8 == 0;
-  const int kr = !vec_k ? 0 : (p.nk <= 256 ? 4 : (p.nk <= 1024 ? 16 : 0));
+  const size_t tiled = tiled_lds(D, p.nk, vec_k);
+  // Generic path: per-wave LDS slice of nk keys + the query row, up to 4
+  // waves (rows) per workgroup.
   const size_t per_wave = ((size_t)p.nk + D) * 4;
   int waves = (int)(65536 / per_wave);
   waves = waves < 1 ? 1 : (waves > 4 ? 4 : waves);
-  const size_t lds = per_wave * waves;
-  dim3 grid((unsigned)((p.nq + waves - 1) / waves), (unsigned)(B * NH));
-  dim3 block((unsigned)(64 * waves));
+  const int rows = tiled ? 4 : waves;
+  const size_t lds = tiled ? tiled : per_wave * waves;
+  dim3 grid((unsigned)((p.nq + rows - 1) / rows), (unsigned)(B * NH));
+  dim3 block((unsigned)(tiled ? 256 : 64 * waves));
   hipStream_t s = static_cast<hipStream_t>(stream);
   clear_launch_error();
 #define LI_MASK_LAUNCH(E_, D_)                                                                          \
   do {                                                                                                  \
-    if (kr == 4)                                                                                        \
-      hipLaunchKernelGGL((block_mask_kernel<E_, D_, 4>), grid, block, lds, s, a, waves);              \
-    else if (kr == 16)                                                                                  \
-      hipLaunchKernelGGL((block_mask_kernel<E_, D_, 16>), grid, block, lds, s, a, waves);             \
+    if (tiled && p.nk <= 256)                                                                           \
+      hipLaunchKernelGGL((block_mask_tiled_kernel<E_, D_, kTiledKt, 4>), grid, block, lds, s, a);      \
+    else if (tiled && p.nk <= 1024)                                                                     \
+      hipLaunchKernelGGL((block_mask_tiled_kernel<E_, D_, kTiledKt, 16>), grid, block, lds, s, a);     \
+    else if (tiled)                                                                                     \
+      hipLaunchKernelGGL((block_mask_tiled_kernel<E_, D_, kTiledKt, 28>), grid, block, lds, s, a);     \
     else                                                                                                \
-      hipLaunchKernelGGL((block_mask_kernel<E_, D_, 0>), grid, block, lds, s, a, waves);              \
+      hipLaunchKernelGGL((block_mask_kernel<E_, D_>), grid, block, lds, s, a, waves);                 \
   } while (0)
   if (dtype == LI_DTYPE_BF16 && D == 128)
     LI_MASK_LAUNCH(Bf16, 128);
