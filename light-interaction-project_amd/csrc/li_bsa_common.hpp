@@ -61,6 +61,10 @@ struct BsaArgs {
   // Optional dispatch order of the whole tiles (a permutation of
   // [0, n_full)): position p of the XCD-aware unit order runs tile order[p].
   const int32_t* order;
+  // XCD chunk: 0 gives each XCD one contiguous range of positions; C > 0
+  // (n_full a multiple of 8 C) deals chunks of C positions round-robin over
+  // the XCDs, so the tiles in flight at once span about 8 C positions.
+  int32_t xchunk;
   // e4m3 kernel only: q and k hold e4m3 codes (1 byte per element) with one
   // fp32 scale per 128-row tile, (B*NH, nqt) and (B*NH, nkb) contiguous.
   const float* q_scale;
@@ -74,8 +78,14 @@ struct BsaArgs {
 // positions; a.order, when given, names the tile at each position.
 __device__ __forceinline__ int unit_tile(const BsaArgs& a, int id) {
   const int xcd = id & 7, slot = id >> 3;
-  const int per = a.n_full >> 3, rem = a.n_full & 7;
-  const int pos = xcd * per + (xcd < rem ? xcd : rem) + slot;
+  int pos;
+  if (a.xchunk > 0) {
+    const int c = a.xchunk;
+    pos = ((slot / c) * 8 + xcd) * c + slot % c;
+  } else {
+    const int per = a.n_full >> 3, rem = a.n_full & 7;
+    pos = xcd * per + (xcd < rem ? xcd : rem) + slot;
+  }
   if (!a.order) return pos;
   const int t = __builtin_amdgcn_readfirstlane(a.order[pos]);
   return t < 0 ? 0 : (t >= a.n_full ? a.n_full - 1 : t);

@@ -219,3 +219,21 @@ def test_balanced_order_gives_the_same_bits(dev):
     err = np.abs(out_b.float().cpu().numpy() - o_ref).max()
     print(f"[gpu]   balanced vs oracle: max abs err {err:.3e}", flush=True)
     assert err <= TOL
+
+
+def test_balanced_order_per_head_chunks(dev):
+    """With B*H a multiple of the 8 XCDs the balanced order sorts and dispatches one head's tiles per chunk: still
+    the same bits as whole tiles in natural order."""
+    bs, D, B, H, nq, nkb = 128, 128, 2, 4, 21, 30
+    Lq, Lk = nq * bs, nkb * bs
+    print(f"[gpu] bsa balanced order, per-head chunks B={B} H={H} nq={nq}", flush=True)
+    rng = np.random.default_rng(23)
+    q, k, v = _inputs(47, B, H, Lq, Lk, D)
+    ind, cnt = _random_lists(rng, B, H, nq, nkb, nkb)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    ii, cc = torch.from_numpy(ind).to(dev), torch.from_numpy(cnt).to(dev)
+    scale = 1.0 / math.sqrt(D)
+    out_b = _core.bsa_forward(qd, kd, vd, ii, cc, scale, bs, balance=True)
+    out_w = _core.bsa_forward(qd, kd, vd, ii, cc, scale, bs, split=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out_b.view(torch.int16), out_w.view(torch.int16))
