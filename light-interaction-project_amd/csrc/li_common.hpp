@@ -32,7 +32,12 @@ struct Bf16 {
 struct F16 {
   typedef f16x8 vec8;
   static __device__ __forceinline__ float to_f32(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+  // The empty asm keeps x an fp32 value: otherwise the compiler may fold the
+  // multiply-add that produced x into the conversion (v_fma_mixlo_f16), one
+  // rounding of the exact result where the arithmetic asks for two (fp32, then
+  // half), which differs at half-way cases.
   static __device__ __forceinline__ uint16_t from_f32(float x) {
+    asm("" : "+v"(x));
     _Float16 h = (_Float16)x;
     return __builtin_bit_cast(uint16_t, h);
   }

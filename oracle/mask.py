@@ -20,7 +20,12 @@ Rounding model (the reference computes these with bf16 torch ops):
 * dot: ``sim = bf16(sum_d q*k)`` (ar_sparse_operation.py:256).
 
 Every fp32 sum over d is sequential from +0.0 in increasing d (bf16*bf16
-products are exact in fp32, so fused and unfused multiply-add agree).  The
+products are exact in fp32, so fused and unfused multiply-add agree).
+
+float16 pools (``fmt="f16"``) follow the same model with every bf16 rounding
+replaced by an IEEE half rounding (the reference's ops then run in float16);
+the normaliser's floor becomes f16(1e-12) = 0.  f16*f16 products are exact in
+fp32 as well.  The
 reference's own sum order (cuBLAS) is not observable; rows whose k-th and
 (k+1)-th non-forced scores are at least two bf16 ulps apart ("tie-free") are
 insensitive to it.
@@ -49,6 +54,21 @@ from .bf16 import bf16_order_key, bf16_to_f32, f32_to_bf16
 METRICS = ("cosine", "scaled_dot_product", "dot")
 
 
+def f16_to_f32(bits):
+    """uint16 IEEE half bit patterns -> float32 values (exact)."""
+    return np.asarray(bits, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def f32_to_f16(x):
+    """float32 -> uint16 IEEE half bit patterns, round to nearest even (numpy's cast)."""
+    with np.errstate(over="ignore"):
+        return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+# element format -> (bits to float32, float32 to bits)
+FORMATS = {"bf16": (bf16_to_f32, f32_to_bf16), "f16": (f16_to_f32, f32_to_f16)}
+
+
 def _seq_dot(a, b):
     """Sequential fp32 dot over the last axis: a (..., M, D), b (..., N, D) -> (..., M, N)."""
     D = a.shape[-1]
@@ -58,29 +78,32 @@ def _seq_dot(a, b):
     return acc
 
 
-def _normalize_bits(x_bits):
-    """bf16 F.normalize(x, dim=-1) with fp32 internals (sequential sum of squares)."""
-    x = bf16_to_f32(x_bits)
+def _normalize_bits(x_bits, fmt="bf16"):
+    """F.normalize(x, dim=-1) in the element format with fp32 internals (sequential sum of squares)."""
+    to32, from32 = FORMATS[fmt]
+    x = to32(x_bits)
     D = x.shape[-1]
     ss = np.zeros(x.shape[:-1], dtype=np.float32)
     for d in range(D):
         ss = ss + x[..., d] * x[..., d]
-    nrm = bf16_to_f32(f32_to_bf16(np.sqrt(ss)))
-    eps = bf16_to_f32(f32_to_bf16(np.float32(1e-12)))
+    nrm = to32(from32(np.sqrt(ss)))
+    eps = to32(from32(np.float32(1e-12)))
     den = np.maximum(nrm, eps)
-    return f32_to_bf16(x / den[..., None])
+    with np.errstate(divide="ignore", invalid="ignore"):
+        return from32(x / den[..., None])
 
 
-def similarity(q_pool_bits, k_pool_bits, metric):
-    """Pooled block similarity (B,H,Nq,D) x (B,H,Nk,D) -> uint16 bf16 scores (B,H,Nq,Nk)."""
+def similarity(q_pool_bits, k_pool_bits, metric, fmt="bf16"):
+    """Pooled block similarity (B,H,Nq,D) x (B,H,Nk,D) -> uint16 scores (B,H,Nq,Nk) in the element format."""
+    to32, from32 = FORMATS[fmt]
     if metric == "cosine":
-        qn, kn = _normalize_bits(q_pool_bits), _normalize_bits(k_pool_bits)
-        return f32_to_bf16(_seq_dot(bf16_to_f32(qn), bf16_to_f32(kn)))
-    dot = f32_to_bf16(_seq_dot(bf16_to_f32(q_pool_bits), bf16_to_f32(k_pool_bits)))
+        qn, kn = _normalize_bits(q_pool_bits, fmt), _normalize_bits(k_pool_bits, fmt)
+        return from32(_seq_dot(to32(qn), to32(kn)))
+    dot = from32(_seq_dot(to32(q_pool_bits), to32(k_pool_bits)))
     if metric == "scaled_dot_product":
         d = q_pool_bits.shape[-1]
         scale = np.float32(1.0 / math.sqrt(d))
-        return f32_to_bf16(bf16_to_f32(dot) * scale)
+        return from32(to32(dot) * scale)
     return dot
 
 
@@ -152,7 +175,8 @@ def budgets(forced, ratio, *, mode, min_budget=None, row_budget=None):
 def select_rows(score_bits, forced, k):
     """Per-row selection -> list of ascending int arrays.
 
-    score_bits (nq, nk) uint16; forced (nq, nk) bool; k (nq,) totals.
+    score_bits (nq, nk) uint16 (bf16 or f16 patterns: both order as sign and
+    magnitude); forced (nq, nk) bool; k (nq,) totals.
     Forced blocks always; then the top ``k - nf`` non-forced by score, ties to the lower index.
     """
     key = bf16_order_key(score_bits)
@@ -170,7 +194,7 @@ def select_rows(score_bits, forced, k):
 
 
 def tie_free(score_bits, forced, k, margin=2):
-    """True for rows whose k-th and (k+1)-th largest non-forced scores are >= margin bf16 ulps apart."""
+    """True for rows whose k-th and (k+1)-th largest non-forced scores are >= margin ulps apart (bf16 or f16)."""
     key = bf16_order_key(score_bits)
     nq = score_bits.shape[0]
     res = np.ones(nq, dtype=bool)
@@ -199,9 +223,9 @@ def assemble(rows_per_bh, num_txt_blk, kmax=None):
     return ind, cnt
 
 
-def build_indices(q_pool_bits, k_pool_bits, *, metric, forced, k, num_txt_blk, kmax=None):
+def build_indices(q_pool_bits, k_pool_bits, *, metric, forced, k, num_txt_blk, kmax=None, fmt="bf16"):
     """Full selection for all (b, h): returns (indices, counts, scores, tie_free_mask)."""
-    score = similarity(q_pool_bits, k_pool_bits, metric)
+    score = similarity(q_pool_bits, k_pool_bits, metric, fmt)
     B, H = score.shape[:2]
     rows = [[select_rows(score[b, h], forced, k) for h in range(H)] for b in range(B)]
     ind, cnt = assemble(rows, num_txt_blk, kmax)

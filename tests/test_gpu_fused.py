@@ -19,11 +19,11 @@ from li_sparse.hy.ar_sparse_operation import fast_generate_indices
 pytestmark = pytest.mark.gpu
 
 
-def _qkv(seed, B, H, Lq, Lk, D, layout, text=0):
+def _qkv(seed, B, H, Lq, Lk, D, layout, text=0, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
 
     def mk(L, scale=1.0):
-        x = (torch.randn(B, L, H, D, generator=g) * scale).to(torch.bfloat16)
+        x = (torch.randn(B, L, H, D, generator=g) * scale).to(dtype)
         return x.permute(0, 2, 1, 3) if layout == "blhd" else x.permute(0, 2, 1, 3).contiguous()
 
     q, k, v = mk(Lq, 0.3), mk(Lk), mk(Lk)
@@ -40,21 +40,22 @@ def _select(params, dev, text_len_unused=None):
 
 
 CASES = [
-    # name, B, H, latent (H, W), tile, frames q, frames k, text tokens, layout
-    ("hy_small_blhd", 1, 3, (30, 52), (2, 8, 8), 2, 6, 0, "blhd"),
-    ("hy_small_bhld_text", 2, 2, (30, 52), (2, 8, 8), 3, 5, 300, "bhld"),
-    ("mg_tile_4x4x8", 1, 2, (22, 40), (4, 4, 8), 4, 8, 0, "blhd"),
-    ("odd_frames_edge", 1, 2, (12, 20), (2, 8, 8), 3, 7, 130, "blhd"),
+    # name, B, H, latent (H, W), tile, frames q, frames k, text tokens, layout, dtype
+    ("hy_small_blhd", 1, 3, (30, 52), (2, 8, 8), 2, 6, 0, "blhd", torch.bfloat16),
+    ("hy_small_bhld_text", 2, 2, (30, 52), (2, 8, 8), 3, 5, 300, "bhld", torch.bfloat16),
+    ("mg_tile_4x4x8", 1, 2, (22, 40), (4, 4, 8), 4, 8, 0, "blhd", torch.bfloat16),
+    ("odd_frames_edge", 1, 2, (12, 20), (2, 8, 8), 3, 7, 130, "blhd", torch.bfloat16),
+    ("hy_small_f16_text", 1, 2, (30, 52), (2, 8, 8), 2, 6, 200, "blhd", torch.float16),
 ]
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
 def test_fused_equals_tiled(dev, case):
-    name, B, H, hw, tile, fq, fk, text, layout = case
+    name, B, H, hw, tile, fq, fk, text, layout, dtype = case
     Hh, W = hw
     D = 128
     print(f"[gpu] fused vs tiled {name}", flush=True)
-    q, k, v, kt, vt = _qkv(sum(map(ord, name)), B, H, fq * Hh * W, fk * Hh * W, D, layout, text)
+    q, k, v, kt, vt = _qkv(sum(map(ord, name)), B, H, fq * Hh * W, fk * Hh * W, D, layout, text, dtype)
     q, k, v = q.to(dev), k.to(dev), v.to(dev)
     kt = kt.to(dev) if kt is not None else None
     vt = vt.to(dev) if vt is not None else None

@@ -141,3 +141,31 @@ def test_lds_key_path(dev, metric, case):
     assert np.array_equal(bits(sc), oscore)
     assert np.array_equal(cnt.cpu().numpy(), ocnt)
     assert np.array_equal(ind.cpu().numpy(), oind)
+
+
+@pytest.mark.parametrize("metric", ["cosine", "scaled_dot_product", "dot"])
+@pytest.mark.parametrize("case", ["shared_pool", "generic_strided"])
+def test_float16_pools(dev, metric, case):
+    """float16 pools: scores, lists and counts bit-exact against the oracle's float16 model, on both kernels."""
+    print(f"[gpu] mask float16 {case} metric={metric}", flush=True)
+    rng = np.random.default_rng(sum(map(ord, metric + case)) + 16)
+    D, nh, nw, nt_q, nt_k = 128, 4, 7, 2, 6                 # nq = 56, nk = 168
+    nq, nk = nt_q * nh * nw, nt_k * nh * nw
+    gen = torch.Generator().manual_seed(int(rng.integers(1 << 30)))
+    qp = (torch.randn(1, 3, nq, D, generator=gen) * 0.5).to(torch.float16)
+    kp = (torch.randn(1, 3, nk, D, generator=gen) * 0.5).to(torch.float16)
+    qd, kd = qp.to(dev), kp.to(dev)
+    if case == "generic_strided":
+        kd = kd.transpose(2, 3).contiguous().transpose(2, 3)
+    geo = {"nq_blk": nq, "nk_blk": nk, "nh": nh, "nw": nw}
+    params = {"tile_size": (2, 8, 8), "topk_ratio": 0.3, "force_diag": True, "force_sink": True}
+    forced, kk = oracle_forced(geo, params, "decode")
+    oind, ocnt, oscore, _ = omask.build_indices(bits(qp), bits(kp), metric=metric, forced=forced, k=kk,
+                                                num_txt_blk=0, fmt="f16")
+    ind, cnt, sc = _core.block_mask(qd, kd, metric=metric, budget_mode=_lib.LI_BUDGET_HISTORY, ratio=0.3, nh=nh,
+                                    nw=nw, force_diag=True, force_sink=True, return_scores=True)
+    torch.cuda.synchronize()
+    assert sc.dtype == torch.float16
+    assert np.array_equal(bits(sc), oscore)
+    assert np.array_equal(cnt.cpu().numpy(), ocnt)
+    assert np.array_equal(ind.cpu().numpy(), oind)

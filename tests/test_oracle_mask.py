@@ -9,6 +9,8 @@ import torch
 from oracle import mask as omask
 from oracle.bf16 import bf16_order_key, bf16_to_f32, f32_to_bf16
 
+import torch_ref
+
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "mask_golden.npz")
 
 CASES = {  # name -> (mode, grid (nt_q, nt_k, nh, nw), text_len, params); must match tests/golden/make_golden.py
@@ -180,3 +182,77 @@ def test_ratio_extremes_and_bruteforce_ties():
         cand = [j for j in range(30) if not forced[r, j]]
         cand.sort(key=lambda j: (-v[r, j], j))
         assert np.array_equal(rows[r], np.sort([7] + cand[:8]))
+
+
+def _f16_torch_bits(x):
+    return torch.from_numpy(np.asarray(x, np.float32)).to(torch.float16).view(torch.int16).numpy().view(np.uint16)
+
+
+def test_f16_conversions_match_torch():
+    """The float16 element format: float32 -> half is torch's cast (ties, overflow, subnormals); half -> float32 exact."""
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(200000) * np.exp(rng.uniform(-20, 14, 200000))).astype(np.float32)
+    u = np.array([0x3F801000, 0x3F803000, 0x477FE000, 0x477FF000, 0x477FEFFF, 0x33800000, 0x33000000, 0x33000001,
+                  0x387FC000, 0x80000000, 0x7F800000, 0xFF800000], dtype=np.uint32)
+    x = np.concatenate([x, u.view(np.float32)])
+    assert np.array_equal(omask.f32_to_f16(x), _f16_torch_bits(x))
+    b = np.arange(0, 0x10000, dtype=np.uint32).astype(np.uint16)
+    f = omask.f16_to_f32(b)
+    fin = np.isfinite(f)
+    assert np.array_equal(omask.f32_to_f16(f[fin]), b[fin])
+    # half patterns order like bf16 ones (sign and magnitude): the same key function applies
+    ks = bf16_order_key(b[fin])
+    i, j = np.random.default_rng(6).integers(0, int(fin.sum()), (2, 100000))
+    lt = f[fin][i] < f[fin][j]
+    assert np.all(ks[i][lt] < ks[j][lt])
+
+
+def test_f16_known_answers():
+    """One-hot pools and a 3-4-5 vector in float16: dot ranking, cosine signs, the normaliser and the scale."""
+    D, nq, nk = 64, 2, 12
+    c = np.array([0.5, 3.0, -1.0, 2.0, 0.25, 7.0, 1.5, -4.0, 6.0, 0.75, 5.0, 1.0], dtype=np.float32)
+    q = np.zeros((1, 1, nq, D), np.float32)
+    q[..., 0] = 1.0
+    k = np.zeros((1, 1, nk, D), np.float32)
+    k[0, 0, :, 0] = c
+    qb, kb = omask.f32_to_f16(q), omask.f32_to_f16(k)
+    assert np.array_equal(omask.f16_to_f32(omask.similarity(qb, kb, "dot", "f16"))[0, 0, 0], c)
+    assert np.array_equal(omask.f16_to_f32(omask.similarity(qb, kb, "cosine", "f16"))[0, 0, 0], np.sign(c))
+    s = omask.f16_to_f32(omask.similarity(qb, kb, "scaled_dot_product", "f16"))[0, 0, 0]
+    scale = np.float32(1.0 / math.sqrt(D))
+    assert np.array_equal(s, (c * scale).astype(np.float16).astype(np.float32))
+    ind, cnt, _, _ = omask.build_indices(qb, kb, metric="dot", forced=np.zeros((nq, nk), bool),
+                                         k=np.full(nq, 3), num_txt_blk=0, fmt="f16")
+    assert np.array_equal(ind[0, 0, 0], [5, 8, 10]) and np.all(cnt == 3)
+    v = np.zeros((1, 1, 1, D), np.float32)
+    v[..., :2] = [3.0, 4.0]
+    n = omask.f16_to_f32(omask._normalize_bits(omask.f32_to_f16(v), "f16"))[0, 0, 0, :2]
+    assert np.array_equal(n, np.array([0.6, 0.8], np.float16).astype(np.float32))
+    # f16(1e-12) = 0: a zero vector divides by zero (NaN), as the float16 reference would
+    z = omask._normalize_bits(np.zeros((1, 1, 1, D), np.uint16), "f16")
+    assert np.all(np.isnan(omask.f16_to_f32(z)))
+
+
+@pytest.mark.parametrize("metric", ["cosine", "scaled_dot_product", "dot"])
+def test_f16_similarity_vs_torch_half(metric):
+    """Scores of the float16 model against the reference's own torch calls run in float16 on the CPU: within one
+    half ulp everywhere (the matmul sum order is the only freedom), equal selections on tie-free rows."""
+    rng = np.random.default_rng(len(metric))
+    B, H, nq, nk, D = 1, 2, 6, 40, 128
+    q = (rng.standard_normal((B, H, nq, D)) * 0.5).astype(np.float32)
+    k = (rng.standard_normal((B, H, nk, D)) * 0.5).astype(np.float32)
+    qb, kb = omask.f32_to_f16(q), omask.f32_to_f16(k)
+    ours = omask.similarity(qb, kb, metric, "f16")
+    qt = torch.from_numpy(omask.f16_to_f32(qb)).to(torch.float16)
+    kt = torch.from_numpy(omask.f16_to_f32(kb)).to(torch.float16)
+    theirs = torch_ref.sim(qt, kt, metric).contiguous().view(torch.int16).numpy().view(np.uint16)
+    d = np.abs(bf16_order_key(ours).astype(np.int64) - bf16_order_key(theirs).astype(np.int64))
+    assert d.max() <= 1
+    forced = np.zeros((nq, nk), bool)
+    kk = np.full(nq, 9)
+    for h in range(H):
+        mine = omask.select_rows(ours[0, h], forced, kk)
+        ref = omask.select_rows(theirs[0, h], forced, kk)
+        tf = omask.tie_free(ours[0, h], forced, kk) & omask.tie_free(theirs[0, h], forced, kk)
+        for r in np.nonzero(tf)[0]:
+            assert np.array_equal(mine[r], ref[r])
