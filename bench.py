@@ -38,7 +38,7 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="hy")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=16, help="heads timed for the CPU baseline sample")
@@ -73,6 +73,18 @@ def event_loop(fn, iters, stream):
     wall = (time.perf_counter() - t0) * 1e3 / iters
     per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     return wall, per
+
+
+def wall_loop(fn, iters):
+    """Wall-clock ms per call over ``iters`` back-to-back calls, bracketed by device synchronisation."""
+    import torch
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / iters
 
 
 def mean(xs):
@@ -135,7 +147,12 @@ def main():
 
     for _ in range(args.warmup):
         step()
-    step_ms, per_step = event_loop(step, args.steps, stream)
+    # Timed region: exactly `steps` calls, bracketed by device synchronisation,
+    # with nothing else enqueued between them.
+    step_ms = wall_loop(step, args.steps)
+    # Per-call GPU times from events around each call, in a loop of their own:
+    # the event records add a few microseconds per call to the wall clock.
+    _, per_step = event_loop(step, args.steps, stream)
 
     # The same call with the key side of the fixed context frames (all K frames
     # before the query chunk) kept in a ContextCache: steps 2.. of a chunk's
@@ -148,8 +165,9 @@ def main():
         cache = ContextCache()
         cparams = dict(params, context_cache=cache, context_frames=ctx_frames)
         cstep = lambda: run_sparse_attention(qd, empty, empty, kd, vd, 1, wl.latent_hw, cparams)  # noqa: E731
-        cstep()
-        c_ms, _ = event_loop(cstep, args.steps, stream)
+        for _ in range(5):
+            cstep()
+        c_ms = wall_loop(cstep, args.steps)
         cached = {"ms_per_call": round(c_ms, 4), "context_frames": ctx_frames,
                   "note": "wall clock per call with the key side of the first context_frames K frames taken from "
                           "a warm ContextCache (the chunk frames are prepared every call)"}
