@@ -109,11 +109,12 @@ def test_five_d_input_and_ties(dev):
 
 
 @pytest.mark.parametrize("metric", ["cosine", "scaled_dot_product", "dot"])
-@pytest.mark.parametrize("case", ["nk_above_shared_path", "strided_pools", "shared_path_partial_tiles"])
+@pytest.mark.parametrize("case", ["nk_above_shared_path", "strided_pools", "shared_path_partial_tiles",
+                                  "shared_path_long_rows"])
 def test_lds_key_path(dev, metric, case):
     """Both mask kernels: the generic one for more key blocks than the shared-pool kernel's LDS holds (nk = 1960 at
     D = 128) and for pool views without a unit d stride; the shared-pool one with a partial last tile and a last
-    workgroup with fewer query rows than waves (D = 64)."""
+    workgroup with fewer query rows than waves (D = 64), and with nk = 1120 (nine tiles, the widest key registers)."""
     print(f"[gpu] mask LDS path {case} metric={metric}", flush=True)
     rng = np.random.default_rng(sum(map(ord, metric + case)))
     D = 128
@@ -121,8 +122,10 @@ def test_lds_key_path(dev, metric, case):
         nh, nw, nt_q, nt_k = 4, 7, 1, 70           # nk = 1960
     elif case == "strided_pools":
         nh, nw, nt_q, nt_k = 3, 5, 2, 6            # nk = 90
-    else:
+    elif case == "shared_path_partial_tiles":
         nh, nw, nt_q, nt_k, D = 3, 5, 2, 13, 64    # nq = 30, nk = 195
+    else:
+        nh, nw, nt_q, nt_k = 4, 7, 1, 40           # nq = 28, nk = 1120
     nq, nk = nt_q * nh * nw, nt_k * nh * nw
     gen = torch.Generator().manual_seed(int(rng.integers(1 << 30)))
     qp = torch.randn(1, 2, nq, D, generator=gen).to(torch.bfloat16)
