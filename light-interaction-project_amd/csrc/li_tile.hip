@@ -59,6 +59,17 @@ __device__ __forceinline__ void store8(uint16_t* p, int64_t stride, bool vec, u3
   }
 }
 
+// Workgroup -> (tile block, b*h) for a (blocks, B*NH) grid, heads fastest in
+// dispatch order: the workgroups in flight together read the same tokens of
+// every head, which with (B, L, H, D) token views is one contiguous span per
+// token instead of one head's 2*D bytes of it.
+__device__ __forceinline__ void tile_unit(int& blk, int& bh) {
+  const uint64_t nbh = gridDim.y;
+  const uint64_t lin = blockIdx.x + (uint64_t)gridDim.x * blockIdx.y;
+  blk = (int)(lin / nbh);
+  bh = (int)(lin - (uint64_t)blk * nbh);
+}
+
 // VEC: every row of the source and the tiles is moved with 16-byte vector
 // accesses (unit innermost stride, 16-byte aligned rows).  The element-wise
 // path for other strides is a separate instantiation, so the vector one does
@@ -69,8 +80,8 @@ __global__ __launch_bounds__(256, VEC ? 4 : 1) void gather_pool_kernel(GatherArg
   constexpr int NG = 256 / CPR;
   __shared__ float red[NG][D];
 
-  const int blk = blockIdx.x;
-  const int bh = blockIdx.y;
+  int blk, bh;
+  tile_unit(blk, bh);
   const int b = bh / a.NH, h = bh % a.NH;
   const int tid = threadIdx.x;
   const int c = tid % CPR, g0 = tid / CPR;
@@ -166,8 +177,8 @@ __global__ __launch_bounds__(256, VEC ? 4 : 1) void gather_fp8_kernel(GatherArgs
   __shared__ float red[NG][D];
   __shared__ uint32_t wmax[4];
 
-  const int blk = blockIdx.x;
-  const int bh = blockIdx.y;
+  int blk, bh;
+  tile_unit(blk, bh);
   const int b = bh / a.NH, h = bh % a.NH;
   const int tid = threadIdx.x;
   const int c = tid % CPR, g0 = tid / CPR;
@@ -282,8 +293,8 @@ template <int D, bool VEC>
 __global__ __launch_bounds__(256) void untile_kernel(UntileArgs a) {
   constexpr int CPR = D / 8;
   constexpr int NG = 256 / CPR;
-  const int blk = blockIdx.x;
-  const int bh = blockIdx.y;
+  int blk, bh;
+  tile_unit(blk, bh);
   const int b = bh / a.NH, h = bh % a.NH;
   const int tid = threadIdx.x;
   const int c = tid % CPR, g0 = tid / CPR;
