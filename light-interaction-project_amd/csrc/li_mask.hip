@@ -189,8 +189,7 @@ __device__ __forceinline__ void load_query(const MaskArgs& a, int b, int h, int 
   }
 }
 
-// Step 1b/2 for one (row, block): score bits from the fp32 dot product, the
-// forced flag, and the order key (0 for a forced block).
+// A query row's position in the key grid, for the forced-block tests.
 struct RowGeom {
   int nk, qb, pos, hw, pt, ph, pw;
   __device__ RowGeom(const li_mask_params& p, int qb_) : nk(p.nk), qb(qb_) {
@@ -202,6 +201,8 @@ struct RowGeom {
   }
 };
 
+// Step 1b/2 for one (row, block): score bits from the fp32 dot product, the
+// forced flag, and the order key (0 for a forced block).
 template <typename E>
 __device__ __forceinline__ uint32_t finish_key(const li_mask_params& p, const RowGeom& g, uint16_t* srow, int j,
                                                float dot, bool& f) {
