@@ -23,12 +23,13 @@
 // 4. the selected blocks are written in ascending order by a ballot/prefix
 //    compaction over j, which replaces the reference's topk + sort.
 //
-// One wave per query row: every per-row reduction is a ballot + popcount
-// inside the wave, and the row's 32-bit keys live in LDS (4 bytes per key
-// block).  Aligned pools with a unit d stride take the shared-pool kernel (4
-// rows of one head per workgroup, the head's pool streamed once through LDS
-// tiles); other pools and very long key grids take the generic kernel, in which
-// each wave reads the pool rows itself.
+// One wave selects each query row: every per-row reduction is a ballot +
+// popcount inside that wave, and the row's 32-bit keys live in LDS (4 bytes
+// per key block).  Aligned pools with a unit d stride take the shared-pool
+// kernel (4 rows of one head per workgroup, two waves scoring each row, the
+// head's pool streamed once through LDS tiles); other pools and very long key
+// grids take the generic kernel, in which each wave scores its row by reading
+// the pool rows itself.
 #include "li_common.hpp"
 
 namespace li {
@@ -271,77 +272,83 @@ __global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a, int waves) 
 }
 
 // Shared-pool path (16-byte aligned pools with unit d stride): a workgroup
-// holds 4 query rows of one (b, h), one per wave, and streams the head's pool
-// through LDS in tiles of 64 KT blocks, so each pool row is read from memory
-// once per 4 query rows.  Rows are padded by 16 bytes in LDS so that lanes
-// reading consecutive blocks hit distinct banks.  For cosine, thread t
-// computes the normaliser of block t of the tile and the whole workgroup then
-// divides the tile in place before the dot
-// products.  Per (row, block) the arithmetic is the generic path's: the same
-// sequential fp32 sum over d of the same operands.  The next tile's loads are
-// in flight while the current one is scored, and the selection keeps the
-// row's keys in registers (nk <= 64 KS).
-template <typename E, int D, int KT, int KS>
-__global__ __launch_bounds__(256) void block_mask_tiled_kernel(MaskArgs a) {
-  constexpr int NT = 64 * KT;     // blocks per tile
-  constexpr int RS = 2 * D + 16;  // LDS row stride in bytes
-  constexpr int CH = D / 8;       // 16-byte chunks per pool row
-  constexpr int PF = NT * CH / 256;  // 16-byte chunks per thread per tile
-  static_assert(PF * 256 == NT * CH, "tile must split evenly over the workgroup");
+// holds 4 query rows of one (b, h), two waves per row, and streams the head's
+// pool through LDS in tiles of 128 blocks, so each pool row is read from
+// memory once per 4 query rows.  Wave (row, half) scores blocks 64 half +
+// lane of every tile against its row's query vector, held in registers.
+// Rows are padded by 16 bytes in LDS so that lanes reading consecutive
+// blocks hit distinct banks.  For cosine, thread t computes the normaliser of
+// block t of the tile and the whole workgroup then divides the tile in place
+// before the dot products.  Per (row, block) the arithmetic is the generic
+// path's: the same sequential fp32 sum over d of the same operands.  The next
+// tile's loads are in flight while the current one is scored, and the first
+// wave of each row then selects with the row's keys in registers
+// (nk <= 64 KS).
+template <typename E, int D, int KS>
+__global__ __launch_bounds__(512) void block_mask_tiled_kernel(MaskArgs a) {
+  constexpr int NT = 128;          // blocks per tile: one per lane of a row's two waves
+  constexpr int NTHR = 512;
+  constexpr int RS = 2 * D + 16;   // LDS row stride in bytes
+  constexpr int CH = D / 8;        // 16-byte chunks per pool row
+  constexpr int PF = NT * CH / NTHR;  // 16-byte chunks per thread per tile
+  static_assert(PF * NTHR == NT * CH, "tile must split evenly over the workgroup");
   extern __shared__ __attribute__((aligned(16))) uint32_t smem[];
+  const li_mask_params& p = a.p;
+  const int nk = p.nk;
   uint8_t* ktile = reinterpret_cast<uint8_t*>(smem);
   float* qall = reinterpret_cast<float*>(ktile + NT * RS);
   float* dn = qall + 4 * D;  // cosine normalisers of the tile's blocks
   uint32_t* kall = reinterpret_cast<uint32_t*>(dn + NT);
-  const li_mask_params& p = a.p;
-  const int nk = p.nk;
+  int* nf2 = reinterpret_cast<int*>(kall + (size_t)4 * nk);  // forced counts of the second waves
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int qb = blockIdx.x * 4 + wave;
+  const int row = wave & 3, half = wave >> 2;
+  const int qb = blockIdx.x * 4 + row;
   const bool live = qb < p.nq;  // dead waves still take part in the tile loads and barriers
   const int bh = blockIdx.y, b = bh / a.NH, h = bh % a.NH;
   const bool cosine = p.metric == LI_METRIC_COSINE;
-  float* qv = qall + wave * D;
-  uint32_t* keys = kall + (size_t)wave * nk;
-  if (live) load_query<E, D>(a, b, h, qb, cosine, qv, lane);
+  float* qv = qall + row * D;
+  uint32_t* keys = kall + (size_t)row * nk;
+  if (live && half == 0) load_query<E, D>(a, b, h, qb, cosine, qv, lane);
 
   const RowGeom g(p, qb);
   const uint16_t* kbase = a.kp + b * a.ks[0] + h * a.ks[1];
   uint16_t* srow = (a.scores && live) ? a.scores + ((int64_t)bh * p.nq + qb) * nk : nullptr;
-  // Chunk i of this thread: tile row tid / CH + i * (256 / CH), column tid % CH.
+  // Chunk i of this thread: tile row tid / CH + i * (NTHR / CH), column tid % CH.
   const int r0 = tid / CH, cc = tid % CH;
   u32x4 pf[PF];
   auto fetch = [&](int j0) LI_MASK_INLINE {
     const int nt = nk - j0 < NT ? nk - j0 : NT;
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      const int r = r0 + i * (256 / CH);
+      const int r = r0 + i * (NTHR / CH);
       if (r < nt) pf[i] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)(j0 + r) * a.ks[2] + 8 * cc);
     }
   };
+  fetch(0);
+  __syncthreads();  // the query rows are visible to both waves of their row
   // The query row in registers for the dot products (wave-uniform values;
   // stale on dead waves, never used there).
   float qr[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) qr[d] = qv[d];
   int nf = 0;
-  fetch(0);
   for (int j0 = 0; j0 < nk; j0 += NT) {
     const int nt = nk - j0 < NT ? nk - j0 : NT;
     __syncthreads();  // the previous tile is consumed
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      const int r = r0 + i * (256 / CH);
+      const int r = r0 + i * (NTHR / CH);
       if (r < nt) *reinterpret_cast<u32x4*>(ktile + r * RS + 16 * cc) = pf[i];
     }
     __syncthreads();
     if (j0 + NT < nk) fetch(j0 + NT);
     if (cosine) {
       if (tid < nt) {
-        uint8_t* row = ktile + tid * RS;
+        uint8_t* krow = ktile + tid * RS;
         float ss = 0.0f;
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
-          const u32x4 w = *reinterpret_cast<const u32x4*>(row + 16 * c);
+          const u32x4 w = *reinterpret_cast<const u32x4*>(krow + 16 * c);
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
             const float x = E::to_f32(uint16_t((w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu));
@@ -357,7 +364,7 @@ __global__ __launch_bounds__(256) void block_mask_tiled_kernel(MaskArgs a) {
       // the chunks it stored.
 #pragma unroll
       for (int i = 0; i < PF; ++i) {
-        const int r = r0 + i * (256 / CH);
+        const int r = r0 + i * (NTHR / CH);
         if (r < nt) {
           u32x4* at = reinterpret_cast<u32x4*>(ktile + r * RS + 16 * cc);
           u32x4 w = *at;
@@ -374,32 +381,26 @@ __global__ __launch_bounds__(256) void block_mask_tiled_kernel(MaskArgs a) {
       __syncthreads();
     }
     if (live) {
-      // Rows past nt hold stale data; their sums are computed and dropped, so
-      // the LDS reads carry no branch and can be issued ahead.
-      float dot[KT];
-#pragma unroll
-      for (int i = 0; i < KT; ++i) dot[i] = 0.0f;
+      // Tile rows past nt hold stale data; their sums are computed and
+      // dropped, so the LDS reads carry no branch and can be issued ahead.
+      const int jl = lane + 64 * half;
+      float dot = 0.0f;
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(ktile + jl * RS + 16 * c);
 #pragma unroll
-        for (int i = 0; i < KT; ++i) {
-          const u32x4 w = *reinterpret_cast<const u32x4*>(ktile + (lane + 64 * i) * RS + 16 * c);
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            dot[i] = dot[i] + qr[8 * c + e] * E::to_f32(uint16_t((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu));
-        }
+        for (int e = 0; e < 8; ++e)
+          dot = dot + qr[8 * c + e] * E::to_f32(uint16_t((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu));
       }
-#pragma unroll
-      for (int i = 0; i < KT; ++i) {
-        const int jl = lane + 64 * i;
-        bool f = false;
-        if (jl < nt) keys[j0 + jl] = finish_key<E>(p, g, srow, j0 + jl, dot[i], f);
-        nf += wave_count(f);
-      }
+      bool f = false;
+      if (jl < nt) keys[j0 + jl] = finish_key<E>(p, g, srow, j0 + jl, dot, f);
+      nf += wave_count(f);
     }
   }
-  if (!live) return;
-  __builtin_amdgcn_wave_barrier();
+  if (half == 1 && lane == 0) nf2[row] = nf;
+  __syncthreads();  // both halves' keys and the second halves' counts are in LDS
+  if (!live || half == 1) return;
+  nf += nf2[row];
   uint32_t kr[KS];
 #pragma unroll
   for (int r = 0; r < KS; ++r) {
@@ -409,14 +410,12 @@ __global__ __launch_bounds__(256) void block_mask_tiled_kernel(MaskArgs a) {
   select_row<KS>(a, [&](int r) LI_MASK_INLINE { return kr[r]; }, KS, nf, qb, bh, lane);
 }
 
-constexpr int kTiledKt = 2;
 constexpr int kTiledMaxNk = 64 * 28;
 
 // LDS bytes of the shared-pool path, or 0 when it does not apply.
 size_t tiled_lds(int D, int nk, bool vec_k) {
   if (!vec_k || nk > kTiledMaxNk) return 0;
-  const size_t bytes =
-      (size_t)64 * kTiledKt * (2 * D + 16 + 4) + (size_t)4 * D * 4 + (size_t)4 * nk * 4;
+  const size_t bytes = (size_t)128 * (2 * D + 16 + 4) + (size_t)4 * D * 4 + (size_t)4 * nk * 4 + 4 * 4;
   return bytes <= 65536 ? bytes : 0;
 }
 
@@ -465,17 +464,17 @@ extern "C" int li_block_mask(int dtype, int32_t B, int32_t NH, int32_t D, const 
   const int rows = tiled ? 4 : waves;
   const size_t lds = tiled ? tiled : per_wave * waves;
   dim3 grid((unsigned)((p.nq + rows - 1) / rows), (unsigned)(B * NH));
-  dim3 block((unsigned)(tiled ? 256 : 64 * waves));
+  dim3 block((unsigned)(tiled ? 512 : 64 * waves));
   hipStream_t s = static_cast<hipStream_t>(stream);
   clear_launch_error();
 #define LI_MASK_LAUNCH(E_, D_)                                                                          \
   do {                                                                                                  \
     if (tiled && p.nk <= 256)                                                                           \
-      hipLaunchKernelGGL((block_mask_tiled_kernel<E_, D_, kTiledKt, 4>), grid, block, lds, s, a);      \
+      hipLaunchKernelGGL((block_mask_tiled_kernel<E_, D_, 4>), grid, block, lds, s, a);                 \
     else if (tiled && p.nk <= 1024)                                                                     \
-      hipLaunchKernelGGL((block_mask_tiled_kernel<E_, D_, kTiledKt, 16>), grid, block, lds, s, a);     \
+      hipLaunchKernelGGL((block_mask_tiled_kernel<E_, D_, 16>), grid, block, lds, s, a);                \
     else if (tiled)                                                                                     \
-      hipLaunchKernelGGL((block_mask_tiled_kernel<E_, D_, kTiledKt, 28>), grid, block, lds, s, a);     \
+      hipLaunchKernelGGL((block_mask_tiled_kernel<E_, D_, 28>), grid, block, lds, s, a);                \
     else                                                                                                \
       hipLaunchKernelGGL((block_mask_kernel<E_, D_>), grid, block, lds, s, a, waves);                 \
   } while (0)
