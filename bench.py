@@ -128,7 +128,7 @@ def main():
     import numpy as np
     import torch
 
-    from li_sparse import _core, _pipeline
+    from li_sparse import _core, _lib, _pipeline
     from li_sparse.hy.ar_sparse_operation import fast_generate_indices, run_sparse_attention
     from li_sparse.workloads import WORKLOADS, make_qkv
 
@@ -182,6 +182,15 @@ def main():
     _core.q_prep(qd, q_t, q_p, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
     _core.kv_prep(kd, vd, k_all, v_all, k_p, 0, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
     ind, cnt = fast_generate_indices(q_p, k_p, 0, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), params, dev)
+    # Rows whose selection cannot change with the score sum order (k-th and (k+1)-th non-forced scores two
+    # ulps apart or more): the same selection again with its scores, and the forced set of the same rules.
+    n_recent = _pipeline.recent_blocks(params, g.tt, g.nh, g.nw, g.nk_blk)
+    ex = _pipeline.extras(params)
+    _, _, sc = _core.block_mask(q_p, k_p, metric=params.get("sim_metric", "cosine"), budget_mode=_lib.LI_BUDGET_HISTORY,
+                                ratio=params.get("topk_ratio", 1.0), nh=g.nh, nw=g.nw, n_recent=n_recent,
+                                return_scores=True, **ex)
+    forced = _core.forced_blocks(g.nq_blk, g.nk_blk, g.nh, g.nw, n_recent, ex["force_diag"], ex["force_sink"])
+    tie_free = _core.tie_free_fraction(sc, cnt, forced)
     torch.cuda.synchronize()
     counts = cnt.cpu().numpy()
     flops = float(counts.sum()) * 4.0 * bs * bs * D
@@ -310,7 +319,7 @@ def main():
         "config": {"workload": wl.note, "batch": B, "heads": H, "head_dim": D, "lq": wl.lq, "lk": wl.lk,
                    "tile": list(wl.tile), "keep_ratio": wl.ratio, "block_size": bs, "nq_blocks": g.nq_blk,
                    "nk_blocks": g.nk_blk, "kept_blocks_per_row_mean": round(float(counts.mean()), 2),
-                   "parallelism": "single GPU"},
+                   "tie_free_rows": round(tie_free, 4), "parallelism": "single GPU"},
         "context_cached": cached,
         "ms_per_call_gpu": {"mean": round(mean(per_step), 4), "median": round(pct(per_step, 50), 4),
                             "p10": round(pct(per_step, 10), 4), "p90": round(pct(per_step, 90), 4),

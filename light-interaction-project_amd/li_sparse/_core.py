@@ -254,6 +254,11 @@ def untile(src, dst, T, H, W, tt, th, tw, nh, nw):
 # ----------------------------------------------------------------------------
 def forced_counts(nq, nk, nh, nw, n_recent=0, diag=False, sink=False, neighbors=False):
     """Number of forced key blocks for every query row (same rules as the mask kernel)."""
+    return forced_blocks(nq, nk, nh, nw, n_recent, diag, sink, neighbors).sum(axis=1)
+
+
+def forced_blocks(nq, nk, nh, nw, n_recent=0, diag=False, sink=False, neighbors=False):
+    """Boolean (nq, nk) forced-block mask (same rules as the mask kernel)."""
     qb = np.arange(nq)
     pos = nk - nq + qb
     j = np.arange(nk)
@@ -271,7 +276,7 @@ def forced_counts(nq, nk, nh, nw, n_recent=0, diag=False, sink=False, neighbors=
         dist = (np.abs(p[:, None] // hw - j[None, :] // hw) + np.abs((p[:, None] % hw) // nw - (j[None, :] % hw) // nw)
                 + np.abs(p[:, None] % nw - j[None, :] % nw))
         f |= (dist <= 1) & ok[:, None]
-    return f.sum(axis=1)
+    return f
 
 
 def row_budgets(nf, nk, mode, ratio, min_budget=7, row_budget=None):
@@ -289,6 +294,31 @@ def row_budgets(nf, nk, mode, ratio, min_budget=7, row_budget=None):
             k = min(max(int(nk * ratio), min_budget), nk)
         out[i] = max(k, f)
     return out
+
+
+def tie_free_fraction(scores, counts, forced, num_txt_blk=0, margin=2):
+    """Fraction of rows whose selection does not depend on score ties.
+
+    ``scores`` (..., nq, nk) bf16/f16 block scores as ``block_mask`` returns them, ``counts`` (..., nq) the row
+    lengths, ``forced`` the (nq, nk) forced-block mask.  A row is tie-free when its k-th and (k+1)-th largest
+    non-forced scores are at least ``margin`` ulps apart (or it keeps all or none of them): then any summation order
+    within an ulp selects the same blocks.
+    """
+    b = scores.detach().cpu().contiguous().view(torch.int16).numpy().astype(np.int32) & 0xFFFF
+    key = np.where(b & 0x8000, -(b & 0x7FFF) - 1, b)  # monotone in the value
+    nq, nk = key.shape[-2:]
+    key = key.reshape(-1, nq, nk)
+    cnt = counts.detach().cpu().numpy().reshape(-1, nq) - num_txt_blk
+    nf = forced.sum(axis=1)
+    free = ~forced
+    ok = total = 0
+    for r in range(key.shape[0]):
+        for q in range(nq):
+            kk = int(cnt[r, q]) - int(nf[q])
+            vals = np.sort(key[r, q][free[q]])[::-1]
+            total += 1
+            ok += not (0 < kk < vals.size) or int(vals[kk - 1]) - int(vals[kk]) >= margin
+    return ok / max(total, 1)
 
 
 _MASK_PLANS = {}

@@ -48,3 +48,23 @@ def test_workload_budgets():
     assert np.all(nf == 2) and np.all(k == 51)  # 2 forced + int(166 * 0.3)
     rb = ragged_budgets(56, 8, 200)
     assert min(rb) == 8 and max(rb) == 200 and 0.09 < np.mean(rb) / 896 < 0.115
+
+
+def test_forced_blocks_and_tie_free_fraction_match_oracle():
+    """The bench's tie-free row count (product code) against the oracle's per-row test on random bf16 scores."""
+    import torch
+
+    rng = np.random.default_rng(11)
+    nq, nk, nh, nw = 28, 140, 4, 7
+    for diag, sink, n_recent in [(True, True, 0), (False, False, 28), (True, False, 28)]:
+        forced = _core.forced_blocks(nq, nk, nh, nw, n_recent, diag, sink)
+        assert np.array_equal(forced, omask.forced_mask(nq, nk, nh, nw, n_recent=n_recent, diag=diag, sink=sink))
+        # few distinct values so that ties are common
+        vals = rng.integers(-40, 40, size=(2, nq, nk)).astype(np.float32) / 16.0
+        bits = torch.from_numpy(vals).to(torch.bfloat16)
+        k = omask.budgets(forced, 0.3, mode="history")
+        counts = torch.from_numpy(np.broadcast_to(k, (2, nq)).astype(np.int32).copy())
+        b = bits.view(torch.int16).numpy().view(np.uint16)
+        want = np.mean([omask.tie_free(b[i], forced, k) for i in range(2)])
+        got = _core.tie_free_fraction(bits, counts, forced)
+        assert abs(got - want) < 1e-12 and 0.0 < got < 1.0
