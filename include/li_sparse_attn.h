@@ -98,6 +98,23 @@ int li_pool(int dtype, int32_t B, int32_t NH, int32_t D,
             const li_tile_geom* geom, void* stream);
 
 /*
+ * The query pool and the key pool of one attention call in a single launch:
+ * job 0 (src0, mean0, pool_off0, geom0) and job 1 (src1, ...) as li_pool each,
+ * same bits.  Replaces the two pool calls the reference makes per call, the
+ * launch_q_prep and launch_kv_prep means (HYAR:58-70, 110-122, called at
+ * HYAR:330-361), for the fused path.  When one job has no blocks or their
+ * sources differ in vector access (16-byte aligned unit-stride rows), the
+ * jobs are launched one after the other.
+ */
+int li_pool_pair(int dtype, int32_t B, int32_t NH, int32_t D,
+                 const void* src0, const int64_t src0_strides[4],
+                 void* mean0, const int64_t mean0_strides[4], int64_t pool_off0,
+                 const li_tile_geom* geom0,
+                 const void* src1, const int64_t src1_strides[4],
+                 void* mean1, const int64_t mean1_strides[4], int64_t pool_off1,
+                 const li_tile_geom* geom1, void* stream);
+
+/*
  * Untile scatter.  Replaces launch_untile(src, dst, T, H, W, tt, th, tw, nh, nw)
  * and _fused_untile_kernel (HYAR:127-161, 204-218; MGS:109-140, 168-177).
  *   src (B, NH, nblk, BS, D) tiles, any strides; dst (B, NH, L, D), any strides.

@@ -75,13 +75,11 @@ __device__ __forceinline__ void tile_unit(int& blk, int& bh) {
 // path for other strides is a separate instantiation, so the vector one does
 // not carry its per-element address registers.
 template <typename E, int D, int NT, bool VEC>
-__global__ __launch_bounds__(256, VEC ? 4 : 1) void gather_pool_kernel(GatherArgs a) {
+__device__ __forceinline__ void gather_pool_block(const GatherArgs& a, int blk, int bh) {
   constexpr int CPR = D / 8;
   constexpr int NG = 256 / CPR;
   __shared__ float red[NG][D];
 
-  int blk, bh;
-  tile_unit(blk, bh);
   const int b = bh / a.NH, h = bh % a.NH;
   const int tid = threadIdx.x;
   const int c = tid % CPR, g0 = tid / CPR;
@@ -156,6 +154,27 @@ __global__ __launch_bounds__(256, VEC ? 4 : 1) void gather_pool_kernel(GatherArg
     const float mean = s[0] / (float)a.bs;
     a.mean[b * a.ms[0] + h * a.ms[1] + (blk + a.pool_off) * a.ms[2] + (int64_t)tid * a.ms[3]] = E::from_f32(mean);
   }
+}
+
+template <typename E, int D, int NT, bool VEC>
+__global__ __launch_bounds__(256, VEC ? 4 : 1) void gather_pool_kernel(GatherArgs a) {
+  int blk, bh;
+  tile_unit(blk, bh);
+  gather_pool_block<E, D, NT, VEC>(a, blk, bh);
+}
+
+// Two pools in one launch (the query and key pools of one attention call):
+// tile blocks 0 .. n0 - 1 of the grid pool job a0, the others pool job a1,
+// counted from 0 again.  The jobs share B, NH, D, the element type and the
+// vector flag; sources, geometry, pool buffers and offsets are their own.
+template <typename E, int D, bool VEC>
+__global__ __launch_bounds__(256, VEC ? 4 : 1) void pool_pair_kernel(GatherArgs a0, GatherArgs a1, int32_t n0) {
+  int blk, bh;
+  tile_unit(blk, bh);
+  if (blk < n0)
+    gather_pool_block<E, D, 0, VEC>(a0, blk, bh);
+  else
+    gather_pool_block<E, D, 0, VEC>(a1, blk - n0, bh);
 }
 
 // The same gather with tensor 0 written as OCP e4m3 codes (1 byte per
@@ -335,21 +354,32 @@ int check_geom(const li_tile_geom* g) {
 
 int64_t num_blocks(const li_tile_geom* g) { return (int64_t)((g->T + g->tt - 1) / g->tt) * g->nh * g->nw; }
 
-template <int NT, bool Q8 = false>
-int launch_gather(int dtype, int32_t B, int32_t NH, int32_t D, GatherArgs& a, const li_tile_geom* geom,
-                  hipStream_t stream) {
+// Checks the geometry and fills a's launch fields; nblk = tile blocks (0:
+// nothing to launch, fields unset).
+int gather_setup(int32_t B, int32_t NH, GatherArgs& a, const li_tile_geom* geom, int64_t& nblk) {
+  nblk = 0;
   if (B <= 0 || NH <= 0) return LI_ERR_INVALID_ARG;
   int st = check_geom(geom);
   if (st != LI_OK) return st;
-  const int64_t nblk = num_blocks(geom);
-  if (nblk == 0) return LI_OK;
-  if (nblk > 0x7FFFFFFF || (int64_t)B * NH > 65535) return LI_ERR_SHAPE;
+  const int64_t n = num_blocks(geom);
+  if (n == 0) return LI_OK;
+  if (n > 0x7FFFFFFF || (int64_t)B * NH > 65535) return LI_ERR_SHAPE;
   if ((int64_t)geom->tt * geom->th * geom->tw >= 65536) return LI_ERR_SHAPE;
   a.NH = NH;
   a.bs = geom->tt * geom->th * geom->tw;
   a.g = *geom;
   a.mg_tw = magic16(geom->tw);
   a.mg_th = magic16(geom->th);
+  nblk = n;
+  return LI_OK;
+}
+
+template <int NT, bool Q8 = false>
+int launch_gather(int dtype, int32_t B, int32_t NH, int32_t D, GatherArgs& a, const li_tile_geom* geom,
+                  hipStream_t stream) {
+  int64_t nblk = 0;
+  const int st = gather_setup(B, NH, a, geom, nblk);
+  if (st != LI_OK || nblk == 0) return st;
   dim3 grid((unsigned)nblk, (unsigned)(B * NH));
   if constexpr (Q8) {
     // The block is held in registers: at most 8 rows per thread.
@@ -397,6 +427,61 @@ int launch_gather(int dtype, int32_t B, int32_t NH, int32_t D, GatherArgs& a, co
     return LI_ERR_UNSUPPORTED;
 #undef LI_GATHER_LAUNCH
   return launch_status();
+}
+
+bool pool_supported(int dtype, int32_t D) {
+  return (dtype == LI_DTYPE_BF16 || dtype == LI_DTYPE_F16) && (D == 128 || D == 64);
+}
+
+// Pools a0 (geometry g0) and a1 (g1) in one launch when both have blocks and
+// the same vector flag, else as two launches of the single pool.
+int launch_pool_pair(int dtype, int32_t B, int32_t NH, int32_t D, GatherArgs& a0, const li_tile_geom* g0,
+                     GatherArgs& a1, const li_tile_geom* g1, hipStream_t stream) {
+  int64_t n0 = 0, n1 = 0;
+  int st = gather_setup(B, NH, a0, g0, n0);
+  if (st == LI_OK) st = gather_setup(B, NH, a1, g1, n1);
+  if (st != LI_OK) return st;
+  if (!pool_supported(dtype, D)) return LI_ERR_UNSUPPORTED;
+  if (n0 == 0 || n1 == 0 || a0.vec_src != a1.vec_src || n0 + n1 > 0x7FFFFFFF) {
+    st = launch_gather<0>(dtype, B, NH, D, a0, g0, stream);
+    return st != LI_OK ? st : launch_gather<0>(dtype, B, NH, D, a1, g1, stream);
+  }
+  clear_launch_error();
+  const dim3 grid((unsigned)(n0 + n1), (unsigned)(B * NH));
+  const int32_t n0i = (int32_t)n0;
+#define LI_PAIR_LAUNCH(E_, D_)                                                                   \
+  do {                                                                                          \
+    if (a0.vec_src)                                                                             \
+      hipLaunchKernelGGL((pool_pair_kernel<E_, D_, true>), grid, dim3(256), 0, stream, a0, a1, n0i);  \
+    else                                                                                        \
+      hipLaunchKernelGGL((pool_pair_kernel<E_, D_, false>), grid, dim3(256), 0, stream, a0, a1, n0i); \
+  } while (0)
+  if (dtype == LI_DTYPE_BF16 && D == 128)
+    LI_PAIR_LAUNCH(Bf16, 128);
+  else if (dtype == LI_DTYPE_BF16 && D == 64)
+    LI_PAIR_LAUNCH(Bf16, 64);
+  else if (dtype == LI_DTYPE_F16 && D == 128)
+    LI_PAIR_LAUNCH(F16, 128);
+  else
+    LI_PAIR_LAUNCH(F16, 64);
+#undef LI_PAIR_LAUNCH
+  return launch_status();
+}
+
+// Fills a pool-only job (no tiles written); false on a null pointer or a negative offset.
+bool pool_job(GatherArgs& a, const void* src, const int64_t* ss, void* mean, const int64_t* ms, int64_t pool_off) {
+  if (!src || !mean || !ss || !ms || pool_off < 0) return false;
+  a = GatherArgs{};
+  a.src[0] = static_cast<const uint16_t*>(src);
+  a.dst[0] = nullptr;
+  for (int i = 0; i < 4; ++i) {
+    a.ss[0][i] = ss[i];
+    a.ms[i] = ms[i];
+  }
+  a.mean = static_cast<uint16_t*>(mean);
+  a.pool_off = pool_off;
+  a.vec_src = vec_ok(src, ss, 4);
+  return true;
 }
 
 }  // namespace
@@ -577,4 +662,16 @@ extern "C" int li_kv_prep_fp8(int dtype, int32_t B, int32_t NH, int32_t D, const
   a.vec_src = vec_ok(k_src, k_src_strides, 4) && vec_ok(v_src, v_src_strides, 4);
   a.vec_dst = vec_ok(v_dst, v_dst_strides, 5);
   return launch_gather<2, true>(dtype, B, NH, D, a, geom, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int li_pool_pair(int dtype, int32_t B, int32_t NH, int32_t D, const void* src0,
+                            const int64_t src0_strides[4], void* mean0, const int64_t mean0_strides[4],
+                            int64_t pool_off0, const li_tile_geom* geom0, const void* src1,
+                            const int64_t src1_strides[4], void* mean1, const int64_t mean1_strides[4],
+                            int64_t pool_off1, const li_tile_geom* geom1, void* stream) {
+  GatherArgs a0, a1;
+  if (!pool_job(a0, src0, src0_strides, mean0, mean0_strides, pool_off0) ||
+      !pool_job(a1, src1, src1_strides, mean1, mean1_strides, pool_off1))
+    return LI_ERR_INVALID_ARG;
+  return launch_pool_pair(dtype, B, NH, D, a0, geom0, a1, geom1, static_cast<hipStream_t>(stream));
 }

@@ -177,6 +177,32 @@ def pool(src, mean, pool_off, T, H, W, tt, th, tw, nh, nw):
     check("li_pool", st)
 
 
+def pool_pair(src0, mean0, pool_off0, geom0, src1, mean1, pool_off1, geom1):
+    """Two pools (see li_pool_pair) in one launch; geom = (T, H, W, tt, th, tw, nh, nw) of each job.
+
+    Same values, bit for bit, as ``pool`` on each job.
+    """
+    dev = _device_check(src0, mean0, src1, mean1)
+    _same_dtype(src0, mean0, src1, mean1)
+    B, NH, _, D = src0.shape
+    if tuple(src1.shape[:2]) != (B, NH) or src1.shape[3] != D:
+        raise ValueError(f"pool pair sources {tuple(src0.shape)} and {tuple(src1.shape)} differ in B, NH or D")
+    gs = []
+    for src, mean, off, geo in ((src0, mean0, pool_off0, geom0), (src1, mean1, pool_off1, geom1)):
+        T, H, W, tt, th, tw, nh, nw = geo
+        nblk = num_blocks(T, tt, nh, nw)
+        if src.shape[2] < T * H * W:
+            raise ValueError(f"source length {src.shape[2]} < T*H*W = {T * H * W}")
+        if tuple(mean.shape[:2]) != (B, NH) or mean.shape[2] < nblk + off or mean.shape[3] != D:
+            raise ValueError(f"pool buffer shape {tuple(mean.shape)} does not hold {nblk}+{off} rows of {D}")
+        gs.append(TileGeom(*geo))
+    st = lib.li_pool_pair(dtype_code(src0), B, NH, D, src0.data_ptr(), i64_array(src0.stride()), mean0.data_ptr(),
+                          i64_array(mean0.stride()), int(pool_off0), ctypes.byref(gs[0]), src1.data_ptr(),
+                          i64_array(src1.stride()), mean1.data_ptr(), i64_array(mean1.stride()), int(pool_off1),
+                          ctypes.byref(gs[1]), _stream(dev))
+    check("li_pool_pair", st)
+
+
 def fused_supported(D, tile, latent_hw):
     """Whether li_bsa_fwd_gather covers this shape.
 

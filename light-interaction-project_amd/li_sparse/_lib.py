@@ -16,7 +16,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL below)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libli_sparse_attn.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 LI_OK = 0
 LI_ERR_INVALID_ARG = -1
@@ -90,6 +90,9 @@ SIGNATURES = {
                                          _i64p, _vp, _vp, _i32, ctypes.c_float, _vp, _i64p, _vp, _vp, _i64, _vp]),
     "li_pool": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p, _i64,
                                ctypes.POINTER(TileGeom), _vp]),
+    "li_pool_pair": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p, _i64,
+                                    ctypes.POINTER(TileGeom), _vp, _i64p, _vp, _i64p, _i64,
+                                    ctypes.POINTER(TileGeom), _vp]),
 }
 
 

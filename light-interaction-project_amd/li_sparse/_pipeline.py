@@ -126,11 +126,13 @@ def _pad_text(x, g, text_len):
     return (F.pad(x, (0, 0, 0, pad)) if pad > 0 else x).contiguous()
 
 
-def _k_side(path, k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, dt):
+def _k_side(path, k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, dt, q_pool_job=None):
     """Key-side buffers of one call: text blocks, then the visual blocks from the first uncached frame.
 
     path: "fused" (K pool; padded text K/V), "fused_fp8" (e4m3 K tiles + scales, K pool; padded text V),
     "tiled" (K/V tiles, K pool), "tiled_fp8" (e4m3 K tiles + scales, V tiles, K pool).
+    q_pool_job: (q, q_pool, pool_off, geometry) of the query pool, taken in the same launch as the K pool on
+    the fused path (li_pool_pair), or on its own when there is no K pool to take (every frame cached).
     """
     cache, layer, cframes = ctx if ctx is not None else (None, None, 0)
     cf = min((max(cframes, 0) // g.tt) * g.tt, g.T_k) if cache is not None else 0
@@ -170,7 +172,10 @@ def _k_side(path, k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, d
         tok = first * g.H * g.W
         kv, vv = k_vis[:, :, tok:], v_vis[:, :, tok:]
         geo = (T, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
-        if path == "fused":
+        if path == "fused" and q_pool_job is not None:
+            _core.pool_pair(*q_pool_job, kv, bufs["k_pool"], fb, geo)
+            q_pool_job = None
+        elif path == "fused":
             _core.pool(kv, bufs["k_pool"], fb, *geo)
         elif path == "fused_fp8":
             _core.tile_prep_fp8(kv, bufs["k8"], bufs["k_scale"], bufs["k_pool"], g.num_txt_blk + fb, fb, *geo)
@@ -179,6 +184,9 @@ def _k_side(path, k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, d
         else:
             _core.kv_prep_fp8(kv, vv, bufs["k8"], bufs["k_scale"], bufs["v_all"], bufs["k_pool"], g.num_txt_blk + fb,
                               fb, *geo)
+    if q_pool_job is not None:
+        src, mean, off, qgeo = q_pool_job
+        _core.pool(src, mean, off, *qgeo)
     return bufs
 
 
@@ -191,8 +199,8 @@ def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events
     o_out = torch.empty_like(q)
     _stage(events, "alloc_end")
     _stage(events, "prep_start")
-    _core.pool(q, q_pool, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
-    kb = _k_side("fused", k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, dt)
+    q_job = (q, q_pool, 0, (g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw))
+    kb = _k_side("fused", k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, dt, q_pool_job=q_job)
     _stage(events, "prep_end")
     _stage(events, "index_start")
     indices, counts = select(q_pool, kb["k_pool"], text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
