@@ -75,16 +75,33 @@ def event_loop(fn, iters, stream):
     return wall, per
 
 
-def wall_loop(fn, iters):
-    """Wall-clock ms per call over ``iters`` back-to-back calls, bracketed by device synchronisation."""
+def wall_loop(fn, iters, stream=None):
+    """Times ``iters`` back-to-back calls, bracketed by device synchronisation on both sides.
+
+    Returns (wall ms per call; host ms per call to enqueue them, i.e. until the
+    last call returned, before the closing synchronisation; GPU ms per call
+    between one event recorded before the first call and one after the last on
+    ``stream``, or None).  Host time well below the wall time means the loop is
+    bound by the GPU, not by the host's submission.
+    """
     import torch
 
+    e0 = e1 = None
+    if stream is not None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    if e0 is not None:
+        e0.record(stream)
     for _ in range(iters):
         fn()
+    if e1 is not None:
+        e1.record(stream)
+    t1 = time.perf_counter()
     torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / iters
+    t2 = time.perf_counter()
+    gpu = e0.elapsed_time(e1) / iters if e0 is not None else None
+    return (t2 - t0) * 1e3 / iters, (t1 - t0) * 1e3 / iters, gpu
 
 
 def mean(xs):
@@ -92,6 +109,30 @@ def mean(xs):
 
 
 TRAFFIC_SUMMARIES = {"hy": "bsa_fwd_hy_traffic.md", "hy_fp8": "bsa_fwd_e4m3_hy_traffic.md"}
+
+
+def valid_rows(T, H, W, tile, nh, nw):
+    """Valid (in-grid) token count of every block of a (T, H, W) grid in block order."""
+    import numpy as np
+
+    tt, th, tw = tile
+    nt = -(-T // tt)
+    ct, ch, cw = np.meshgrid(np.arange(nt), np.arange(nh), np.arange(nw), indexing="ij")
+    n = (np.minimum(tt, T - ct * tt) * np.minimum(th, H - ch * th) * np.minimum(tw, W - cw * tw))
+    return n.reshape(-1).astype(np.float64)
+
+
+def valid_token_flops(ind, cnt, g, D, num_txt_blk=0):
+    """4 * D * (valid query rows) * (valid key rows) summed over every kept (query tile, key block) pair."""
+    import numpy as np
+
+    vq = valid_rows(g.T_q, g.H, g.W, (g.tt, g.th, g.tw), g.nh, g.nw)
+    vk = np.concatenate([np.full(num_txt_blk, float(g.bs)), valid_rows(g.T_k, g.H, g.W, (g.tt, g.th, g.tw), g.nh,
+                                                                       g.nw)])
+    kmax = ind.shape[-1]
+    keep = np.arange(kmax)[None, None, None, :] < cnt[..., None]
+    rows_k = np.where(keep, vk[np.clip(ind, 0, vk.size - 1)], 0.0).sum(axis=-1)   # (B, H, nq)
+    return float((rows_k * vq[None, None, :]).sum()) * 4.0 * D
 
 
 def load_traffic(kernel, workload):
@@ -145,13 +186,19 @@ def main():
     def step():
         return run_sparse_attention(qd, empty, empty, kd, vd, 1, wl.latent_hw, params)
 
-    for _ in range(args.warmup):
-        step()
+    def warm(fn):
+        # The same --warmup count of untimed calls before every timed loop.
+        for _ in range(args.warmup):
+            fn()
+
+    warm(step)
     # Timed region: exactly `steps` calls, bracketed by device synchronisation,
-    # with nothing else enqueued between them.
-    step_ms = wall_loop(step, args.steps)
+    # with nothing else enqueued between them (one event before and one after
+    # the loop give the GPU's own time for it).
+    step_ms, submit_ms, step_gpu_ms = wall_loop(step, args.steps, stream)
     # Per-call GPU times from events around each call, in a loop of their own:
     # the event records add a few microseconds per call to the wall clock.
+    warm(step)
     _, per_step = event_loop(step, args.steps, stream)
 
     # The same call with the key side of the fixed context frames (all K frames
@@ -165,9 +212,8 @@ def main():
         cache = ContextCache()
         cparams = dict(params, context_cache=cache, context_frames=ctx_frames)
         cstep = lambda: run_sparse_attention(qd, empty, empty, kd, vd, 1, wl.latent_hw, cparams)  # noqa: E731
-        for _ in range(5):
-            cstep()
-        c_ms = wall_loop(cstep, args.steps)
+        warm(cstep)
+        c_ms, _, _ = wall_loop(cstep, args.steps)
         cached = {"ms_per_call": round(c_ms, 4), "context_frames": ctx_frames,
                   "note": "wall clock per call with the key side of the first context_frames K frames taken from "
                           "a warm ContextCache (the chunk frames are prepared every call)"}
@@ -193,6 +239,7 @@ def main():
     torch.cuda.synchronize()
     counts = cnt.cpu().numpy()
     flops = float(counts.sum()) * 4.0 * bs * bs * D
+    flops_valid = valid_token_flops(ind.cpu().numpy(), counts, g, D)
     qf, kf, vf = q_t.flatten(2, 3), k_all.flatten(2, 3), v_all.flatten(2, 3)
     scale = 1.0 / math.sqrt(D)
     fp8 = bool(params.get("qk_fp8", False))
@@ -226,15 +273,13 @@ def main():
                         fp8_tiles=(q8, qs, k8, ks) if fp8 else None)
         return
 
-    # Warm-up long enough for the clocks to settle after the host-side set-up above.
-    for _ in range(20):
-        attn()
+    warm(attn)
     _, attn_per = event_loop(attn, args.steps, stream)
     attn_ms = mean(attn_per)   # average launch duration (events on the launch stream)
     attn_tflops = flops / (attn_ms * 1e-3) / 1e12
     tiled_info = None
     if fused or fp8:
-        tiled_attn()
+        warm(tiled_attn)
         _, tiled_per = event_loop(tiled_attn, max(5, args.steps // 5), stream)
         tiled_ms = mean(tiled_per)
         tiled_info = {"ms": round(tiled_ms, 4), "tflops": round(flops / (tiled_ms * 1e-3) / 1e12, 2),
@@ -242,7 +287,7 @@ def main():
                               "the same attention on pre-gathered tiles (the unfused sequence's kernel)"}
     tiled_fp8_info = None
     if fp8 and fused:
-        tiled_fp8()
+        warm(tiled_fp8)
         _, t8_per = event_loop(tiled_fp8, max(5, args.steps // 5), stream)
         t8_ms = mean(t8_per)
         tiled_fp8_info = {"ms": round(t8_ms, 4), "tflops": round(flops / (t8_ms * 1e-3) / 1e12, 2),
@@ -250,8 +295,7 @@ def main():
 
     # Dense comparators: torch SDPA (valid tokens) and this kernel with every block kept.
     sdpa = lambda: torch.nn.functional.scaled_dot_product_attention(qd, kd, vd)  # noqa: E731
-    for _ in range(3):
-        sdpa()
+    warm(sdpa)
     _, dense_per = event_loop(sdpa, max(5, args.steps // 5), stream)
     dense_ms = mean(dense_per)
     dense_flops = 4.0 * wl.lq * wl.lk * D * H * B
@@ -265,7 +309,7 @@ def main():
     if _core.dense_supported(qd, kd, vd):
         # This library's dense kernel (li_attn_fwd_dense) on the same valid tokens.
         own = lambda: _core.attn_dense(qd, kd, vd)  # noqa: E731
-        own()
+        warm(own)
         _, own_per = event_loop(own, max(5, args.steps // 5), stream)
         own_ms = mean(own_per)
         dense.update({"own_dense_kernel_ms": round(own_ms, 4),
@@ -276,7 +320,7 @@ def main():
         all_ind = torch.arange(g.nk_blk, dtype=torch.int32, device=dev).expand(B, H, g.nq_blk, g.nk_blk).contiguous()
         all_cnt = torch.full((B, H, g.nq_blk), g.nk_blk, dtype=torch.int32, device=dev)
         full = lambda: _core.bsa_forward(qf, kf, vf, all_ind, all_cnt, scale, bs)  # noqa: E731
-        full()
+        warm(full)
         _, full_per = event_loop(full, max(5, args.steps // 5), stream)
         full_ms = mean(full_per)
         full_flops = float(B * H * g.nq_blk * g.nk_blk) * 4.0 * bs * bs * D
@@ -311,11 +355,17 @@ def main():
     result = {
         "metric": "sparse-attn fwd ms/call + TFLOPS (% MFMA peak) at HY shape, 30% keep",
         "value": round(flops / (step_ms * 1e-3) / 1e12, 2),
+        "value_valid_tokens": round(flops_valid / (step_ms * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(step_ms, 4),
+        "timed_loop": {"host_submit_ms_per_step": round(submit_ms, 4), "gpu_ms_per_step": round(step_gpu_ms, 4),
+                       "warmup_calls_before_every_timed_loop": args.warmup,
+                       "note": "host_submit = host time to enqueue the K timed calls (until the last call "
+                               "returned, before the closing synchronisation); gpu = one event before and one "
+                               "after the K calls on the launch stream"},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -332,7 +382,13 @@ def main():
         "attention_kernel": {"kernel": kname, "ms": round(attn_ms, 4), "median_ms": round(pct(attn_per, 50), 4),
                              "tflops": round(attn_tflops, 2),
                              "pct_bf16_peak": round(100.0 * attn_tflops / PEAK_BF16_TFLOPS, 2),
-                             "retained_gflop": round(flops / 1e9, 2)},
+                             "retained_gflop": round(flops / 1e9, 2),
+                             "retained_gflop_valid_tokens": round(flops_valid / 1e9, 2),
+                             "tflops_valid_tokens": round(flops_valid / (attn_ms * 1e-3) / 1e12, 2),
+                             "flop_bases": "retained_gflop (value, roofline) counts every row of each kept 128x128 "
+                                           "tile pair, padding rows included (the kernel computes them); "
+                                           "*_valid_tokens counts valid query rows x valid key rows only, the "
+                                           "basis of the dense comparators' gflop_valid_tokens"},
         ("attention_kernel_bf16" if fp8 else "attention_kernel_tiled"): tiled_info,
         "attention_kernel_e4m3_tiled": tiled_fp8_info,
         "dense_comparator": dense,
@@ -342,7 +398,10 @@ def main():
                      "peak_note": ("half the FLOPs (Q K^T) at the 5.0 PFLOP/s fp8 peak, half (P V) at the "
                                    "2.5 PFLOP/s bf16 peak") if fp8 else "dense bf16 MFMA peak",
                      "traffic": load_traffic(kname, args.workload),
-                     "traffic_unit": "bytes per launch (HBM/MALL side, rocprofv3 FETCH_SIZE + WRITE_SIZE)"},
+                     "traffic_unit": "bytes per launch (HBM/MALL side, rocprofv3 FETCH_SIZE + WRITE_SIZE)",
+                     "traffic_source": (f"read from profiles/{TRAFFIC_SUMMARIES[args.workload]} (committed "
+                                        "rocprofv3 --pmc summary of `bench.py --profile`), not measured in this "
+                                        "run") if args.workload in TRAFFIC_SUMMARIES else None},
         "fused_path": fused,
         "prep_bytes_per_call": prep_bytes,
     }

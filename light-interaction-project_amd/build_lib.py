@@ -8,6 +8,7 @@ package that loads it.
 """
 import argparse
 import concurrent.futures
+import hashlib
 import os
 import subprocess
 import sys
@@ -17,6 +18,8 @@ REPO = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "li_sparse", "libli_sparse_attn.so")
+# Hash of the sources and flags the library was built from, written next to it.
+STAMP = OUT + ".stamp"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -29,6 +32,28 @@ CFLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
 ]
+
+
+def source_hash():
+    """sha256 over the HIP sources, the C header and the compile flags."""
+    h = hashlib.sha256(" ".join(CFLAGS).encode())
+    inc = os.path.join(REPO, "include")
+    files = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".hpp", ".h"))]
+    files += [os.path.join(inc, f) for f in os.listdir(inc) if f.endswith(".h")]
+    for path in sorted(files):
+        h.update(os.path.relpath(path, REPO).encode())
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+def is_current():
+    """Whether the built library exists and was built from the current sources."""
+    try:
+        with open(STAMP) as f:
+            return os.path.exists(OUT) and f.read().strip() == source_hash()
+    except OSError:
+        return False
 
 
 def _compile(src):
@@ -51,6 +76,8 @@ def build(jobs=4, verbose=True):
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, OUT)
+    with open(STAMP, "w") as f:
+        f.write(source_hash() + "\n")
     if verbose:
         print(f"built {OUT}")
     return OUT

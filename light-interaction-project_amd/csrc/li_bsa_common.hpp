@@ -91,10 +91,6 @@ __device__ __forceinline__ int unit_tile(const BsaArgs& a, int id) {
   return t < 0 ? 0 : (t >= a.n_full ? a.n_full - 1 : t);
 }
 
-// Launches the 4-wave D = 128, BS = 128 kernel for units [0, a.n_full) whole
-// tiles plus the split half-units (li_bsa_fwd_w4.hip).
-int launch_bsa_w4(int dtype, BsaArgs& a, int units, hipStream_t s);
-
 namespace {
 
 // MFMA row i of the score tile reads K row perm(i): bits 2 and 3 swapped.

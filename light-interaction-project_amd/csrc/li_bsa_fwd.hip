@@ -46,10 +46,7 @@
 //  * Workgroup ids are remapped so that each XCD (ids are dealt round-robin
 //    over the 8 XCDs) processes a contiguous range of (head, tile) work and
 //    the tiles of one head share that XCD's L2 for their K/V blocks.
-#include <cstdlib>
-#include <cstring>
 #include <mutex>
-#include <type_traits>
 
 #include "li_bsa_common.hpp"
 
@@ -1274,27 +1271,9 @@ int launch_bsa(BsaArgs& a, int tiles, hipStream_t s) {
   return launch_status();
 }
 
-// Kernel for D = 128, BS = 128: the 8-wave ping-pong kernel, or the 4-wave
-// kernel (li_bsa_fwd_w4.hip) when the environment variable LI_BSA_WAVES is 4
-// (read on every call).  The 8-wave kernel is the faster one on MI355X at the
-// shapes measured so far.
-bool use_w4() {
-  const char* e = std::getenv("LI_BSA_WAVES");
-  return e && std::strcmp(e, "4") == 0;
-}
-
-template <typename E>
-int launch_w4(BsaArgs& a, int tiles, hipStream_t s) {
-  const int nsplit = tiles - a.n_full;
-  clear_launch_error();
-  launch_bsa_w4(std::is_same<E, Bf16>::value ? LI_DTYPE_BF16 : LI_DTYPE_F16, a, a.n_full + 2 * nsplit, s);
-  if (nsplit > 0) hipLaunchKernelGGL(bsa_merge_kernel<E>, dim3(4 * nsplit), dim3(256), 0, s, a);
-  return launch_status();
-}
-
 template <typename E>
 int dispatch_bsa(BsaArgs& a, int bs, int D, int tiles, hipStream_t s) {
-  if (bs == 128 && D == 128) return use_w4() ? launch_w4<E>(a, tiles, s) : launch_bsa_dma<E, 128>(a, tiles, s);
+  if (bs == 128 && D == 128) return launch_bsa_dma<E, 128>(a, tiles, s);
   if (bs == 128 && D == 64) return launch_bsa<E, 128, 64>(a, tiles, s);
   if (bs == 64 && D == 128) return launch_bsa_dma<E, 64>(a, tiles, s);
   if (bs == 64 && D == 64) return launch_bsa<E, 64, 64>(a, tiles, s);

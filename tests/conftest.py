@@ -14,10 +14,11 @@ LIB = os.path.join(PKG_DIR, "li_sparse", "libli_sparse_attn.so")
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a ROCm GPU (MI355X); runs the HIP kernels")
-    # Build the native library only when nothing is built yet.
-    if not os.path.exists(LIB):
-        import build_lib
+    # (Re)build the native library when it is missing or was built from other
+    # sources (the hash of csrc/ and include/ recorded by the build differs).
+    import build_lib
 
+    if not build_lib.is_current():
         build_lib.build(jobs=4, verbose=False)
 
 

@@ -46,19 +46,10 @@ def _f64(t):
     return t.double().numpy() if t.dtype != torch.bfloat16 else bf16_to_f32(bits(t)).astype(np.float64)
 
 
-@pytest.fixture(params=["8", "4"])
-def waves(request, monkeypatch):
-    """Kernel choice for D=128/BS=128 (LI_BSA_WAVES, read by the library on every call)."""
-    monkeypatch.setenv("LI_BSA_WAVES", request.param)
-    return request.param
-
-
 @pytest.mark.parametrize("bs,D", [(128, 128), (128, 64), (64, 128), (64, 64)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_random_lists_vs_oracle(dev, bs, D, dtype, waves):
-    if waves == "4" and (bs, D) != (128, 128):
-        pytest.skip("the 4-wave kernel exists for D=128, BS=128 only")
-    print(f"[gpu] bsa bs={bs} D={D} {dtype} waves={waves}", flush=True)
+def test_random_lists_vs_oracle(dev, bs, D, dtype):
+    print(f"[gpu] bsa bs={bs} D={D} {dtype}", flush=True)
     rng = np.random.default_rng(bs + D)
     B, H, nq, nkb = 1, 3, 5, 9
     Lq, Lk = nq * bs - 17, nkb * bs          # ragged last query tile
@@ -78,7 +69,7 @@ def test_random_lists_vs_oracle(dev, bs, D, dtype, waves):
     assert np.abs(lse_g[fin] - lse_ref[fin]).max() < 1e-3
 
 
-def test_full_hy_shape_sampled_tiles(dev, waves):
+def test_full_hy_shape_sampled_tiles(dev):
     print("[gpu] bsa full HY shape (B=1, H=16, Lq=7168, Lk=21504, 51 blocks/row)", flush=True)
     bs, D, H = 128, 128, 16
     nq, nkb, kk = 56, 168, 51
@@ -98,7 +89,7 @@ def test_full_hy_shape_sampled_tiles(dev, waves):
     assert err <= TOL
 
 
-def test_tail_split_matches_whole_tiles_and_oracle(dev, waves):
+def test_tail_split_matches_whole_tiles_and_oracle(dev):
     """Tiles of a partial last round run as two halves of their block list plus a merge kernel."""
     from li_sparse import _lib
 

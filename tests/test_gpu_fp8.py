@@ -4,8 +4,9 @@
   oracle (oracle.fp8.quantize_blocks over oracle.tile.tile_gather);
 * attention on e4m3 Q/K: against the float64 oracle on the dequantized Q/K
   (max abs error <= 2e-2, LSE within 1e-3), whole / split / balanced;
-* the whole call: against the oracle pipeline with ``qk_fp8`` and against the
-  bf16 call on the same inputs (the fp8 error budget, FP8_VS_BF16).
+* the whole call: against the oracle pipeline with ``qk_fp8``, against the
+  bf16 call on the same inputs (FP8_VS_BF16) and against the bf16 reference
+  output, the float64 oracle on the unquantized bf16 inputs (FP8_VS_BF16_REF).
 """
 import math
 
@@ -27,6 +28,8 @@ from oracle.geometry import block_geometry
 pytestmark = pytest.mark.gpu
 TOL = 2e-2          # bf16 output vs the float64 oracle on the same (dequantized) Q/K
 FP8_VS_BF16 = 1e-2  # e4m3 call vs bf16 call, max abs, HY shape (measured 3.9e-3; mean abs 6.9e-5)
+# e4m3 call vs the bf16 reference output (the float64 oracle on the bf16 Q/K/V), max abs, HY shape
+FP8_VS_BF16_REF = 1e-2
 
 
 def _codes(t):
@@ -238,6 +241,23 @@ def test_fp8_call_vs_bf16_call_hy_shape(dev):
         err = max(err, np.abs(got[b, h, rows] - ref["out"][b, h, rows]).max())
     print(f"[gpu]   vs oracle over {len(tiles)} sampled tiles {err:.3e}", flush=True)
     assert err <= TOL
+    # The e4m3 call against the bf16 reference output: the float64 oracle on the bf16 inputs (qk_fp8 off,
+    # so Q and K are not quantized), on more sampled tiles.
+    tiles16 = tiles + [(0, int(h), int(m)) for h, m in zip(rng.integers(0, wl.heads, 12), rng.integers(0, nq, 12))]
+    ref16 = oracle_pipeline(q, k, v, wl.latent_hw, WORKLOADS["hy"].sparse_params(), heads=tiles16)
+    assert np.array_equal(ref16["indices"], ref["indices"])   # the selection does not see the quantization
+    err16 = mean16 = 0.0
+    n16 = 0
+    for b, h, m in tiles16:
+        rows = ref16["perm"][m * bs:(m + 1) * bs]
+        rows = rows[rows >= 0]
+        dd = np.abs(got[b, h, rows] - ref16["out"][b, h, rows])
+        err16 = max(err16, dd.max())
+        mean16 += dd.sum()
+        n16 += dd.size
+    print(f"[gpu]   vs the bf16 reference output over {len(tiles16)} sampled tiles: max abs {err16:.3e}, "
+          f"mean abs {mean16 / n16:.3e}", flush=True)
+    assert err16 <= FP8_VS_BF16_REF
 
 
 def test_fp8_rejects_unsupported(dev):
