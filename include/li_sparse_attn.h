@@ -35,7 +35,7 @@ enum li_status {
   LI_ERR_INDEX_RANGE = -4,   /* block index out of range (HYK:194-195) */
   LI_ERR_UNSUPPORTED = -5,   /* head_dim / block size / dtype not built */
   LI_ERR_LAUNCH = -6,        /* HIP launch error */
-  LI_ERR_TOO_LARGE = -7      /* key-block count above the mask builder's limit */
+  LI_ERR_TOO_LARGE = -7      /* above a built-in limit: mask builder key blocks, noalloc scratch */
 };
 
 enum li_dtype { LI_DTYPE_BF16 = 0, LI_DTYPE_F16 = 1 };
@@ -236,6 +236,33 @@ int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D,
                       const int32_t* block_counts, const int64_t cnt_strides[3],
                       float sm_scale, void* out, const int64_t out_strides[4], float* lse,
                       void* workspace, int64_t workspace_bytes, int32_t flags, void* stream);
+
+/*
+ * li_bsa_fwd_gather without a workspace argument and without any device
+ * allocation: the tail split's partials and the LI_BSA_BALANCE tile order go
+ * to a scratch array of li_bsa_fwd_noalloc_scratch_bytes() bytes (32 MiB)
+ * that the library holds on each device it runs on until the process ends.
+ * Same kernels, same split and order decisions and same results, bit for
+ * bit, as li_bsa_fwd_gather given a workspace of li_bsa_fwd_workspace_size()
+ * bytes.  LI_ERR_TOO_LARGE when that workspace would exceed the scratch.
+ * Every call on a device shares that device's scratch: calls that overlap
+ * on one GPU (other streams, other threads) race and must be serialised by
+ * the caller.  No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).
+ */
+int li_bsa_fwd_gather_noalloc(int dtype, int32_t B, int32_t NH, int32_t D,
+                              const void* q, const int64_t q_strides[4],
+                              const void* k, const int64_t k_strides[4],
+                              const void* v, const int64_t v_strides[4],
+                              const void* k_txt, const void* v_txt, int32_t num_txt_blk,
+                              const li_tile_geom* q_geom, const li_tile_geom* k_geom,
+                              const int32_t* block_indices, const int64_t idx_strides[4], int32_t n_cols,
+                              const int32_t* block_counts, const int64_t cnt_strides[3],
+                              float sm_scale, void* out, const int64_t out_strides[4], float* lse,
+                              int32_t flags, void* stream);
+/* Size of the per-device scratch of li_bsa_fwd_gather_noalloc (no counterpart in the reference). */
+int64_t li_bsa_fwd_noalloc_scratch_bytes(void);
 
 /*
  * Workspace bytes li_bsa_fwd / li_bsa_fwd_gather can use for these sizes on

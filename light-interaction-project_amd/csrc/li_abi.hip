@@ -13,7 +13,7 @@ void li::record_launch_error(hipError_t e) {
 
 extern "C" const char* li_last_error(void) { return g_last_error; }
 
-extern "C" int li_abi_version(void) { return 8; }
+extern "C" int li_abi_version(void) { return 9; }
 
 extern "C" const char* li_status_string(int status) {
   switch (status) {
@@ -24,7 +24,7 @@ extern "C" const char* li_status_string(int status) {
     case LI_ERR_INDEX_RANGE: return "Sparse indices out of bounds.";
     case LI_ERR_UNSUPPORTED: return "unsupported head_dim, block size or dtype";
     case LI_ERR_LAUNCH: return "HIP kernel launch failed";
-    case LI_ERR_TOO_LARGE: return "too many key blocks for the mask builder";
+    case LI_ERR_TOO_LARGE: return "size above a built-in limit (mask builder key blocks, or the allocation-free entry point's scratch)";
     default: return "unknown status";
   }
 }

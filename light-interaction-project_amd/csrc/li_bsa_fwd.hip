@@ -1579,6 +1579,68 @@ extern "C" int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D, co
   return launch_bsa_gather<F16>(a, (int)tiles, s);
 }
 
+// Scratch of li_bsa_fwd_gather_noalloc: the tail split's partials or the
+// tile order of LI_BSA_BALANCE (what the workspace of li_bsa_fwd_gather
+// holds).  Each device holds its own copy from module load until the process
+// ends.  Host code must not pass the array's name to a kernel (it is a
+// host-side stand-in); scratch_ptr() gives the device address instead.
+constexpr int64_t kScratchBytes = 32ll << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+namespace {
+
+// Device address of `scratch` on the current device, looked up once per
+// device with hipGetSymbolAddress and cached; null (with the error recorded
+// for li_last_error) when the lookup fails.
+void* scratch_ptr() {
+  static std::mutex mu;
+  static void* ptrs[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      record_launch_error(e != hipSuccess ? e : hipErrorInvalidSymbol);
+      return nullptr;
+    }
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
+}
+
+}  // namespace
+
+extern "C" int li_bsa_fwd_gather_noalloc(int dtype, int32_t B, int32_t NH, int32_t D, const void* q,
+                                         const int64_t q_strides[4], const void* k, const int64_t k_strides[4],
+                                         const void* v, const int64_t v_strides[4], const void* k_txt,
+                                         const void* v_txt, int32_t num_txt_blk, const li_tile_geom* q_geom,
+                                         const li_tile_geom* k_geom, const int32_t* block_indices,
+                                         const int64_t idx_strides[4], int32_t n_cols, const int32_t* block_counts,
+                                         const int64_t cnt_strides[3], float sm_scale, void* out,
+                                         const int64_t out_strides[4], float* lse, int32_t flags, void* stream) {
+  if (dtype != LI_DTYPE_BF16 && dtype != LI_DTYPE_F16) return LI_ERR_UNSUPPORTED;
+  BsaArgs a = {};
+  int64_t tiles = 0;
+  int st = gather_setup(a, tiles, B, NH, D, q, q_strides, k, k_strides, v, v_strides, k_txt, v_txt, num_txt_blk,
+                        q_geom, k_geom, block_indices, idx_strides, n_cols, block_counts, cnt_strides, sm_scale, out,
+                        out_strides, lse, false);
+  if (st != LI_OK || tiles == 0) return st;
+  // The workspace li_bsa_fwd_gather would use for this call must fit the scratch.
+  const int64_t need = li_bsa_fwd_workspace_size(B, NH, a.nqt * 128, D, 128);
+  if (need > kScratchBytes) return LI_ERR_TOO_LARGE;
+  void* ws = scratch_ptr();
+  if (!ws) return LI_ERR_LAUNCH;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  st = plan_units(a, tiles, D, 128, ws, need, flags, s);
+  if (st != LI_OK) return st;
+  if (dtype == LI_DTYPE_BF16) return launch_bsa_gather<Bf16>(a, (int)tiles, s);
+  return launch_bsa_gather<F16>(a, (int)tiles, s);
+}
+
+extern "C" int64_t li_bsa_fwd_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
 extern "C" int li_bsa_fwd_fp8(int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int32_t D, const void* q8,
                               const float* q_scale, const void* k8, const float* k_scale, const void* v,
                               const int32_t* block_indices, const int64_t idx_strides[4], int32_t n_cols,

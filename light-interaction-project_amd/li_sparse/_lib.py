@@ -16,7 +16,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL below)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libli_sparse_attn.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 LI_OK = 0
 LI_ERR_INVALID_ARG = -1
@@ -77,6 +77,11 @@ SIGNATURES = {
     "li_bsa_fwd_gather": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
                                          _i32, ctypes.POINTER(TileGeom), ctypes.POINTER(TileGeom), _vp, _i64p, _i32,
                                          _vp, _i64p, ctypes.c_float, _vp, _i64p, _vp, _vp, _i64, _i32, _vp]),
+    "li_bsa_fwd_gather_noalloc": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+                                                 _vp, _vp, _i32, ctypes.POINTER(TileGeom), ctypes.POINTER(TileGeom),
+                                                 _vp, _i64p, _i32, _vp, _i64p, ctypes.c_float, _vp, _i64p, _vp, _i32,
+                                                 _vp]),
+    "li_bsa_fwd_noalloc_scratch_bytes": (ctypes.c_int64, []),
     "li_tile_prep_fp8": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
                                         _i64, _i64, ctypes.POINTER(TileGeom), _vp]),
     "li_kv_prep_fp8": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
