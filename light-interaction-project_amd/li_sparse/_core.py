@@ -1,19 +1,33 @@
-"""Torch-facing launchers over the C ABI (device memory and streams come from torch).
+"""Torch-facing launchers: host-side validation, then one ``torch.ops.li`` operator each.
 
-Every function validates shapes on the host, then enqueues one HIP kernel on
-torch's current stream of the tensors' device.  Nothing here synchronises the
-stream or computes on the CPU.
+Every function validates shapes on the host with the reference's error
+types and messages, then calls its custom operator (li_sparse/_ops.py, a C++
+layer over the C ABI) which enqueues the HIP kernel on torch's current stream
+of the tensors' device.  Nothing here synchronises the stream or computes on
+the CPU.
 """
-import ctypes
 import math
+import re
 
 import numpy as np
 import torch
 
 from . import _lib
-from ._lib import MaskParams, TileGeom, check, i64_array, lib
+from ._ops import ops
 
 _DTYPES = {torch.bfloat16: _lib.LI_DTYPE_BF16, torch.float16: _lib.LI_DTYPE_F16}
+_STATUS = re.compile(r"(li_\w+) failed: .*\(status (-?\d+)\)")
+
+
+def _run(op, *args):
+    """Calls a torch.ops.li operator; a failed C-ABI status becomes LiError (with its status code)."""
+    try:
+        return op(*args)
+    except RuntimeError as e:
+        m = _STATUS.search(str(e))
+        if m is None:
+            raise
+        raise _lib.LiError(m.group(1), int(m.group(2))) from None
 METRICS = {"cosine": _lib.LI_METRIC_COSINE, "scaled_dot_product": _lib.LI_METRIC_SCALED_DOT}
 
 
@@ -34,10 +48,6 @@ def _device_check(*ts):
     return dev
 
 
-def _stream(dev):
-    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-
-
 def _same_dtype(*ts):
     for t in ts[1:]:
         if t.dtype != ts[0].dtype:
@@ -54,7 +64,7 @@ def num_blocks(T, tt, nh, nw):
 
 def q_prep(src, dst, mean, T, H, W, tt, th, tw, nh, nw):
     """Tile gather + mean pool of one tensor (see li_q_prep)."""
-    dev = _device_check(src, dst, mean)
+    _device_check(src, dst, mean)
     _same_dtype(src, dst, mean)
     B, NH, L, D = src.shape
     nblk, bs = num_blocks(T, tt, nh, nw), tt * th * tw
@@ -64,16 +74,13 @@ def q_prep(src, dst, mean, T, H, W, tt, th, tw, nh, nw):
         raise ValueError(f"tile buffer shape {tuple(dst.shape)} does not hold {nblk} tiles of ({bs}, {D})")
     if tuple(mean.shape[:2]) != (B, NH) or mean.shape[2] < nblk or mean.shape[3] != D:
         raise ValueError(f"pool buffer shape {tuple(mean.shape)} does not hold {nblk} rows of {D}")
-    g = TileGeom(T, H, W, tt, th, tw, nh, nw)
-    st = lib.li_q_prep(dtype_code(src), B, NH, D, src.data_ptr(), i64_array(src.stride()), dst.data_ptr(),
-                       i64_array(dst.stride()), mean.data_ptr(), i64_array(mean.stride()), ctypes.byref(g),
-                       _stream(dev))
-    check("li_q_prep", st)
+    dtype_code(src)
+    _run(ops.q_prep, src, dst, mean, [T, H, W, tt, th, tw, nh, nw])
 
 
 def kv_prep(k_src, v_src, k_dst, v_dst, k_mean, dst_off, pool_off, T, H, W, tt, th, tw, nh, nw):
     """Tile gather of K and V (at block offset dst_off) + K mean pool (at pool_off) (see li_kv_prep)."""
-    dev = _device_check(k_src, v_src, k_dst, v_dst, k_mean)
+    _device_check(k_src, v_src, k_dst, v_dst, k_mean)
     _same_dtype(k_src, v_src, k_dst, v_dst, k_mean)
     B, NH, L, D = k_src.shape
     if tuple(v_src.shape) != tuple(k_src.shape):
@@ -86,12 +93,9 @@ def kv_prep(k_src, v_src, k_dst, v_dst, k_mean, dst_off, pool_off, T, H, W, tt, 
             raise ValueError(f"{name} shape {tuple(t.shape)} does not hold {nblk}+{dst_off} tiles of ({bs}, {D})")
     if tuple(k_mean.shape[:2]) != (B, NH) or k_mean.shape[2] < nblk + pool_off or k_mean.shape[3] != D:
         raise ValueError(f"pool buffer shape {tuple(k_mean.shape)} does not hold {nblk}+{pool_off} rows")
-    g = TileGeom(T, H, W, tt, th, tw, nh, nw)
-    st = lib.li_kv_prep(dtype_code(k_src), B, NH, D, k_src.data_ptr(), i64_array(k_src.stride()),
-                        v_src.data_ptr(), i64_array(v_src.stride()), k_dst.data_ptr(), i64_array(k_dst.stride()),
-                        v_dst.data_ptr(), i64_array(v_dst.stride()), k_mean.data_ptr(), i64_array(k_mean.stride()),
-                        int(dst_off), int(pool_off), ctypes.byref(g), _stream(dev))
-    check("li_kv_prep", st)
+    dtype_code(k_src)
+    _run(ops.kv_prep, k_src, v_src, k_dst, v_dst, k_mean, int(dst_off), int(pool_off),
+         [T, H, W, tt, th, tw, nh, nw])
 
 
 FP8 = torch.float8_e4m3fn
@@ -115,7 +119,7 @@ def tile_prep_fp8(src, dst, scales, mean, dst_off, pool_off, T, H, W, tt, th, tw
     dst (B, NH, nblk, BS, D) float8_e4m3fn and scales (B, NH, nblk) float32, written at block blk + dst_off;
     mean (or None) as q_prep's pool, at block blk + pool_off.
     """
-    dev = _device_check(src, dst, scales, *([mean] if mean is not None else []))
+    _device_check(src, dst, scales, *([mean] if mean is not None else []))
     B, NH, L, D = src.shape
     dtype_code(src)
     nblk, bs = num_blocks(T, tt, nh, nw), tt * th * tw
@@ -127,18 +131,12 @@ def tile_prep_fp8(src, dst, scales, mean, dst_off, pool_off, T, H, W, tt, th, tw
         _same_dtype(src, mean)
         if tuple(mean.shape[:2]) != (B, NH) or mean.shape[2] < nblk + pool_off or mean.shape[3] != D:
             raise ValueError(f"pool buffer shape {tuple(mean.shape)} does not hold {nblk}+{pool_off} rows of {D}")
-    g = TileGeom(T, H, W, tt, th, tw, nh, nw)
-    st = lib.li_tile_prep_fp8(dtype_code(src), B, NH, D, src.data_ptr(), i64_array(src.stride()), dst.data_ptr(),
-                              i64_array(dst.stride()), scales.data_ptr(), i64_array(scales.stride()),
-                              mean.data_ptr() if mean is not None else None,
-                              i64_array(mean.stride()) if mean is not None else None, int(dst_off), int(pool_off),
-                              ctypes.byref(g), _stream(dev))
-    check("li_tile_prep_fp8", st)
+    _run(ops.tile_prep_fp8, src, dst, scales, mean, int(dst_off), int(pool_off), [T, H, W, tt, th, tw, nh, nw])
 
 
 def kv_prep_fp8(k_src, v_src, k_dst, k_scales, v_dst, k_mean, dst_off, pool_off, T, H, W, tt, th, tw, nh, nw):
     """kv_prep with K written as e4m3 codes + per-block scales and V copied unchanged (see li_kv_prep_fp8)."""
-    dev = _device_check(k_src, v_src, k_dst, k_scales, v_dst, k_mean)
+    _device_check(k_src, v_src, k_dst, k_scales, v_dst, k_mean)
     _same_dtype(k_src, v_src, v_dst, k_mean)
     B, NH, L, D = k_src.shape
     if tuple(v_src.shape) != tuple(k_src.shape):
@@ -152,18 +150,14 @@ def kv_prep_fp8(k_src, v_src, k_dst, k_scales, v_dst, k_mean, dst_off, pool_off,
         raise ValueError(f"v_dst shape {tuple(v_dst.shape)} does not hold {nblk}+{dst_off} tiles of ({bs}, {D})")
     if tuple(k_mean.shape[:2]) != (B, NH) or k_mean.shape[2] < nblk + pool_off or k_mean.shape[3] != D:
         raise ValueError(f"pool buffer shape {tuple(k_mean.shape)} does not hold {nblk}+{pool_off} rows")
-    g = TileGeom(T, H, W, tt, th, tw, nh, nw)
-    st = lib.li_kv_prep_fp8(dtype_code(k_src), B, NH, D, k_src.data_ptr(), i64_array(k_src.stride()),
-                            v_src.data_ptr(), i64_array(v_src.stride()), k_dst.data_ptr(), i64_array(k_dst.stride()),
-                            k_scales.data_ptr(), i64_array(k_scales.stride()), v_dst.data_ptr(),
-                            i64_array(v_dst.stride()), k_mean.data_ptr(), i64_array(k_mean.stride()), int(dst_off),
-                            int(pool_off), ctypes.byref(g), _stream(dev))
-    check("li_kv_prep_fp8", st)
+    dtype_code(k_src)
+    _run(ops.kv_prep_fp8, k_src, v_src, k_dst, k_scales, v_dst, k_mean, int(dst_off), int(pool_off),
+                    [T, H, W, tt, th, tw, nh, nw])
 
 
 def pool(src, mean, pool_off, T, H, W, tt, th, tw, nh, nw):
     """Tile mean pool without writing tiles (see li_pool); same values as q_prep / kv_prep."""
-    dev = _device_check(src, mean)
+    _device_check(src, mean)
     _same_dtype(src, mean)
     B, NH, L, D = src.shape
     nblk = num_blocks(T, tt, nh, nw)
@@ -171,10 +165,8 @@ def pool(src, mean, pool_off, T, H, W, tt, th, tw, nh, nw):
         raise ValueError(f"source length {L} < T*H*W = {T * H * W}")
     if tuple(mean.shape[:2]) != (B, NH) or mean.shape[2] < nblk + pool_off or mean.shape[3] != D:
         raise ValueError(f"pool buffer shape {tuple(mean.shape)} does not hold {nblk}+{pool_off} rows of {D}")
-    g = TileGeom(T, H, W, tt, th, tw, nh, nw)
-    st = lib.li_pool(dtype_code(src), B, NH, D, src.data_ptr(), i64_array(src.stride()), mean.data_ptr(),
-                     i64_array(mean.stride()), int(pool_off), ctypes.byref(g), _stream(dev))
-    check("li_pool", st)
+    dtype_code(src)
+    _run(ops.pool, src, mean, int(pool_off), [T, H, W, tt, th, tw, nh, nw])
 
 
 def pool_pair(src0, mean0, pool_off0, geom0, src1, mean1, pool_off1, geom1):
@@ -182,7 +174,7 @@ def pool_pair(src0, mean0, pool_off0, geom0, src1, mean1, pool_off1, geom1):
 
     Same values, bit for bit, as ``pool`` on each job.
     """
-    dev = _device_check(src0, mean0, src1, mean1)
+    _device_check(src0, mean0, src1, mean1)
     _same_dtype(src0, mean0, src1, mean1)
     B, NH, _, D = src0.shape
     if tuple(src1.shape[:2]) != (B, NH) or src1.shape[3] != D:
@@ -195,12 +187,9 @@ def pool_pair(src0, mean0, pool_off0, geom0, src1, mean1, pool_off1, geom1):
             raise ValueError(f"source length {src.shape[2]} < T*H*W = {T * H * W}")
         if tuple(mean.shape[:2]) != (B, NH) or mean.shape[2] < nblk + off or mean.shape[3] != D:
             raise ValueError(f"pool buffer shape {tuple(mean.shape)} does not hold {nblk}+{off} rows of {D}")
-        gs.append(TileGeom(*geo))
-    st = lib.li_pool_pair(dtype_code(src0), B, NH, D, src0.data_ptr(), i64_array(src0.stride()), mean0.data_ptr(),
-                          i64_array(mean0.stride()), int(pool_off0), ctypes.byref(gs[0]), src1.data_ptr(),
-                          i64_array(src1.stride()), mean1.data_ptr(), i64_array(mean1.stride()), int(pool_off1),
-                          ctypes.byref(gs[1]), _stream(dev))
-    check("li_pool_pair", st)
+        gs.append([int(x) for x in geo])
+    dtype_code(src0)
+    _run(ops.pool_pair, src0, mean0, int(pool_off0), gs[0], src1, mean1, int(pool_off1), gs[1])
 
 
 def fused_supported(D, tile, latent_hw):
@@ -222,7 +211,7 @@ def bsa_forward_gather(q, k, v, k_txt, v_txt, num_txt_blk, T_q, T_k, H, W, tt, t
     zero-padded (B,NH,num_txt_blk*BS,D) contiguous text keys/values or None.  ``split`` and ``balance``
     as for ``bsa_forward``.  No host sync.
     """
-    dev = _device_check(q, k, v, out, indices, counts)
+    _device_check(q, k, v, out, indices, counts)
     _same_dtype(q, k, v, out)
     B, NH, Lq, D = q.shape
     if indices.dtype != torch.int32 or counts.dtype != torch.int32:
@@ -238,28 +227,17 @@ def bsa_forward_gather(q, k, v, k_txt, v_txt, num_txt_blk, T_q, T_k, H, W, tt, t
         _same_dtype(q, k_txt, v_txt)
         if not (k_txt.is_contiguous() and v_txt.is_contiguous()):
             raise ValueError("padded text K/V must be contiguous")
-    bs = tt * th * tw
-    lse = torch.empty((B, NH, nq * bs), dtype=torch.float32, device=dev) if return_lse else None
-    with torch.cuda.device(dev):
-        ws_bytes = int(lib.li_bsa_fwd_workspace_size(B, NH, nq * bs, D, bs)) if (split or balance) else 0
-    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev) if ws_bytes > 0 else None
-    gq, gk = TileGeom(T_q, H, W, tt, th, tw, nh, nw), TileGeom(T_k, H, W, tt, th, tw, nh, nw)
-    st = lib.li_bsa_fwd_gather(dtype_code(q), B, NH, D, q.data_ptr(), i64_array(q.stride()), k.data_ptr(),
-                               i64_array(k.stride()), v.data_ptr(), i64_array(v.stride()),
-                               k_txt.data_ptr() if num_txt_blk > 0 else None,
-                               v_txt.data_ptr() if num_txt_blk > 0 else None, int(num_txt_blk), ctypes.byref(gq),
-                               ctypes.byref(gk), indices.data_ptr(), i64_array(indices.stride()), indices.shape[3],
-                               counts.data_ptr(), i64_array(counts.stride()), float(sm_scale), out.data_ptr(),
-                               i64_array(out.stride()), lse.data_ptr() if lse is not None else None,
-                               ws.data_ptr() if ws is not None else None, ws_bytes,
-                               _lib.LI_BSA_BALANCE if balance else 0, _stream(dev))
-    check("li_bsa_fwd_gather", st)
+    dtype_code(q)
+    lse = _run(ops.bsa_fwd_gather, q, k, v, k_txt if num_txt_blk > 0 else None,
+               v_txt if num_txt_blk > 0 else None, int(num_txt_blk), [T_q, H, W, tt, th, tw, nh, nw],
+               [T_k, H, W, tt, th, tw, nh, nw], indices, counts, float(sm_scale), out, bool(return_lse), bool(split),
+               bool(balance))
     return (out, lse) if return_lse else out
 
 
 def untile(src, dst, T, H, W, tt, th, tw, nh, nw):
     """Inverse scatter of tiles into the linear token layout (see li_untile)."""
-    dev = _device_check(src, dst)
+    _device_check(src, dst)
     _same_dtype(src, dst)
     B, NH, L, D = dst.shape
     nblk, bs = num_blocks(T, tt, nh, nw), tt * th * tw
@@ -267,10 +245,8 @@ def untile(src, dst, T, H, W, tt, th, tw, nh, nw):
         raise ValueError(f"destination length {L} < T*H*W = {T * H * W}")
     if src.shape[:2] != (B, NH) or src.shape[2] < nblk or src.shape[3:] != (bs, D):
         raise ValueError(f"tile buffer shape {tuple(src.shape)} does not hold {nblk} tiles of ({bs}, {D})")
-    g = TileGeom(T, H, W, tt, th, tw, nh, nw)
-    st = lib.li_untile(dtype_code(src), B, NH, D, src.data_ptr(), i64_array(src.stride()), dst.data_ptr(),
-                       i64_array(dst.stride()), ctypes.byref(g), _stream(dev))
-    check("li_untile", st)
+    dtype_code(src)
+    _run(ops.untile, src, dst, [T, H, W, tt, th, tw, nh, nw])
 
 
 # ----------------------------------------------------------------------------
@@ -397,19 +373,11 @@ def block_mask(q_pool, k_pool, *, metric, budget_mode, ratio, nh, nw, num_txt_bl
     metric_code = METRICS.get(metric, _lib.LI_METRIC_DOT)
     kmax, rb_dev = _mask_plan(dev, nq, nk, nh, nw, num_txt_blk, n_recent, bool(force_diag), bool(force_sink),
                               bool(force_neighbors), budget_mode, float(ratio), int(min_budget), row_budget)
-    indices = torch.empty((B, NH, nq, kmax), dtype=torch.int32, device=dev)
-    counts = torch.empty((B, NH, nq), dtype=torch.int32, device=dev)
-    scores = torch.empty((B, NH, nq, nk), dtype=q_pool.dtype, device=dev) if return_scores else None
-    p = MaskParams(metric=metric_code, budget_mode=budget_mode, topk_ratio=float(ratio), min_budget=int(min_budget),
-                   n_recent=int(n_recent), force_diag=int(bool(force_diag)), force_sink=int(bool(force_sink)),
-                   force_neighbors=int(bool(force_neighbors)), nq=nq, nk=nk, nh=nh, nw=nw,
-                   num_txt_blk=int(num_txt_blk), kmax=kmax,
-                   row_budget=rb_dev.data_ptr() if rb_dev is not None else None,
-                   scale=float(np.float32(1.0 / math.sqrt(D))))
-    st = lib.li_block_mask(dtype_code(q_pool), B, NH, D, q_pool.data_ptr(), i64_array(q_pool.stride()),
-                           k_pool.data_ptr(), i64_array(k_pool.stride()), ctypes.byref(p), indices.data_ptr(),
-                           counts.data_ptr(), scores.data_ptr() if scores is not None else None, _stream(dev))
-    check("li_block_mask", st)
+    dtype_code(q_pool)
+    indices, counts, scores = _run(ops.block_mask, q_pool, k_pool, metric_code, int(budget_mode), float(ratio),
+                                             int(min_budget), int(n_recent), bool(force_diag), bool(force_sink),
+                                             bool(force_neighbors), int(nh), int(nw), int(num_txt_blk), int(kmax),
+                                             rb_dev, bool(return_scores))
     if return_scores:
         return indices, counts, scores
     return indices, counts
@@ -422,7 +390,7 @@ def bsa_forward(q, k, v, indices, counts, sm_scale, block_size, return_lse=False
     ``split=False`` runs every query tile whole (no tail split workspace).  ``balance=True`` (rows of
     unequal length) starts the query tiles longest first instead (LI_BSA_BALANCE; no tail split).
     """
-    dev = _device_check(q, k, v, indices, counts)
+    _device_check(q, k, v, indices, counts)
     _same_dtype(q, k, v)
     if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
         raise ValueError("q, k, v must be contiguous")
@@ -437,23 +405,16 @@ def bsa_forward(q, k, v, indices, counts, sm_scale, block_size, return_lse=False
         raise ValueError(f"block_indices shape {tuple(indices.shape)} does not cover {nqt} query tiles")
     if counts.dim() != 3 or tuple(counts.shape[:2]) != (B, NH) or counts.shape[2] < nqt:
         raise ValueError(f"block_counts shape {tuple(counts.shape)} does not cover {nqt} query tiles")
+    if Lk % block_size != 0:
+        raise ValueError(f"K Length ({Lk}) must be divisible by logical_block_size ({block_size})")
+    dtype_code(q)
     if out is None:
         out = torch.empty_like(q)
-    lse = torch.empty((B, NH, Lq), dtype=torch.float32, device=dev) if return_lse else None
-    # Scratch for splitting the query tiles of a partial last round (through
-    # torch's caching allocator; stream-ordered, so it may be freed on return).
-    with torch.cuda.device(dev):
-        ws_bytes = int(lib.li_bsa_fwd_workspace_size(B, NH, Lq, D, int(block_size))) if (split or balance) else 0
-    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev) if ws_bytes > 0 else None
-    st = lib.li_bsa_fwd(dtype_code(q), B, NH, Lq, Lk, D, q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                        indices.data_ptr(), i64_array(indices.stride()), indices.shape[3], counts.data_ptr(),
-                        i64_array(counts.stride()), float(sm_scale), int(block_size), out.data_ptr(),
-                        lse.data_ptr() if lse is not None else None,
-                        ws.data_ptr() if ws is not None else None, ws_bytes,
-                        _lib.LI_BSA_BALANCE if balance else 0, _stream(dev))
-    if st == _lib.LI_ERR_K_LEN:
-        raise ValueError(f"K Length ({Lk}) must be divisible by logical_block_size ({block_size})")
-    check("li_bsa_fwd", st)
+    # The operator allocates the workspace for splitting the query tiles of a
+    # partial last round (or for the balanced tile order) through torch's
+    # caching allocator; stream-ordered, so it is freed on return.
+    lse = _run(ops.bsa_fwd, q, k, v, indices, counts, float(sm_scale), int(block_size), out, bool(return_lse),
+               bool(split), bool(balance))
     return (out, lse) if return_lse else out
 
 
@@ -487,21 +448,12 @@ def bsa_forward_fp8(q8, q_scale, k8, k_scale, v, indices, counts, sm_scale, bloc
         raise ValueError(f"block_indices shape {tuple(indices.shape)} does not cover {nqt} query tiles")
     if counts.dim() != 3 or tuple(counts.shape[:2]) != (B, NH) or counts.shape[2] < nqt:
         raise ValueError(f"block_counts shape {tuple(counts.shape)} does not cover {nqt} query tiles")
+    if Lk % block_size != 0:
+        raise ValueError(f"K Length ({Lk}) must be divisible by logical_block_size ({block_size})")
     if out is None:
         out = torch.empty((B, NH, Lq, D), dtype=torch.bfloat16, device=dev)
-    lse = torch.empty((B, NH, Lq), dtype=torch.float32, device=dev) if return_lse else None
-    with torch.cuda.device(dev):
-        ws_bytes = int(lib.li_bsa_fwd_workspace_size(B, NH, Lq, D, int(block_size))) if (split or balance) else 0
-    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev) if ws_bytes > 0 else None
-    st = lib.li_bsa_fwd_fp8(B, NH, Lq, Lk, D, q8.data_ptr(), q_scale.data_ptr(), k8.data_ptr(), k_scale.data_ptr(),
-                            v.data_ptr(), indices.data_ptr(), i64_array(indices.stride()), indices.shape[3],
-                            counts.data_ptr(), i64_array(counts.stride()), float(sm_scale), int(block_size),
-                            out.data_ptr(), lse.data_ptr() if lse is not None else None,
-                            ws.data_ptr() if ws is not None else None, ws_bytes,
-                            _lib.LI_BSA_BALANCE if balance else 0, _stream(dev))
-    if st == _lib.LI_ERR_K_LEN:
-        raise ValueError(f"K Length ({Lk}) must be divisible by logical_block_size ({block_size})")
-    check("li_bsa_fwd_fp8", st)
+    lse = _run(ops.bsa_fwd_fp8, q8, q_scale, k8, k_scale, v, indices, counts, float(sm_scale), int(block_size),
+               out, bool(return_lse), bool(split), bool(balance))
     return (out, lse) if return_lse else out
 
 
@@ -513,7 +465,7 @@ def bsa_forward_fp8_gather(q8, q_scale, k8, k_scale, v, v_txt, num_txt_blk, T_q,
     v (B,NH,Lk,D) bf16 token view; v_txt (B,NH,num_txt_blk*128,D) contiguous zero-padded or None;
     out (B,NH,Lq,D) bf16 token view, written at valid tokens.
     """
-    dev = _device_check(q8, q_scale, k8, k_scale, v, indices, counts, out)
+    _device_check(q8, q_scale, k8, k_scale, v, indices, counts, out)
     if q8.dtype != FP8 or k8.dtype != FP8 or v.dtype != torch.bfloat16 or out.dtype != torch.bfloat16:
         raise TypeError("q8/k8 must be float8_e4m3fn, v and out bfloat16")
     if not (q8.is_contiguous() and k8.is_contiguous() and q_scale.is_contiguous() and k_scale.is_contiguous()):
@@ -530,21 +482,9 @@ def bsa_forward_fp8_gather(q8, q_scale, k8, k_scale, v, v_txt, num_txt_blk, T_q,
     if num_txt_blk > 0 and (v_txt is None or not v_txt.is_contiguous()
                             or tuple(v_txt.shape) != (B, NH, num_txt_blk * 128, D)):
         raise ValueError("v_txt must be a contiguous (B, NH, num_txt_blk*128, D) buffer")
-    gq = TileGeom(T_q, H, W, tt, th, tw, nh, nw)
-    gk = TileGeom(T_k, H, W, tt, th, tw, nh, nw)
-    lse = torch.empty((B, NH, nq * 128), dtype=torch.float32, device=dev) if return_lse else None
-    with torch.cuda.device(dev):
-        ws_bytes = int(lib.li_bsa_fwd_workspace_size(B, NH, nq * 128, D, 128))
-    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev) if ws_bytes > 0 else None
-    st = lib.li_bsa_fwd_fp8_gather(B, NH, D, q8.data_ptr(), q_scale.data_ptr(), k8.data_ptr(), k_scale.data_ptr(),
-                                   v.data_ptr(), i64_array(v.stride()),
-                                   v_txt.data_ptr() if v_txt is not None else None, int(num_txt_blk),
-                                   ctypes.byref(gq), ctypes.byref(gk), indices.data_ptr(), i64_array(indices.stride()),
-                                   indices.shape[3], counts.data_ptr(), i64_array(counts.stride()), float(sm_scale),
-                                   out.data_ptr(), i64_array(out.stride()), lse.data_ptr() if lse is not None else None,
-                                   ws.data_ptr() if ws is not None else None, ws_bytes,
-                                   _lib.LI_BSA_BALANCE if balance else 0, _stream(dev))
-    check("li_bsa_fwd_fp8_gather", st)
+    lse = _run(ops.bsa_fwd_fp8_gather, q8, q_scale, k8, k_scale, v, v_txt if num_txt_blk > 0 else None,
+               int(num_txt_blk), [T_q, H, W, tt, th, tw, nh, nw], [T_k, H, W, tt, th, tw, nh, nw], indices, counts,
+               float(sm_scale), out, bool(return_lse), bool(balance))
     return (out, lse) if return_lse else out
 
 
@@ -570,7 +510,7 @@ def attn_dense(q, k, v, k_txt=None, v_txt=None, sm_scale=None, return_lse=False,
     q (B,H,Lq,128), k/v (B,H,Lk,128) token views; k_txt/v_txt (B,H,N_txt,128) or None.  Output has q's strides
     (``empty_like(q)``).  Raises LiError(LI_ERR_UNSUPPORTED) for shapes it is not built for.
     """
-    dev = _device_check(q, k, v)
+    _device_check(q, k, v)
     _same_dtype(q, k, v)
     B, NH, Lq, D = q.shape
     Lk = k.shape[2]
@@ -590,16 +530,6 @@ def attn_dense(q, k, v, k_txt=None, v_txt=None, sm_scale=None, return_lse=False,
         sm_scale = 1.0 / math.sqrt(D)
     if out is None:
         out = torch.empty_like(q)
-    nq = ceil_div(Lq, 128)
-    lse = torch.empty((B, NH, nq * 128), dtype=torch.float32, device=dev) if return_lse else None
-    with torch.cuda.device(dev):
-        ws_bytes = int(lib.li_bsa_fwd_workspace_size(B, NH, nq * 128, D, 128)) if split else 0
-    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev) if ws_bytes > 0 else None
-    st = lib.li_attn_fwd_dense(dtype_code(q), B, NH, D, Lq, Lk, q.data_ptr(), i64_array(q.stride()), k.data_ptr(),
-                               i64_array(k.stride()), v.data_ptr(), i64_array(v.stride()),
-                               kt.data_ptr() if kt is not None else None, vt.data_ptr() if vt is not None else None,
-                               txt_len, float(sm_scale), out.data_ptr(), i64_array(out.stride()),
-                               lse.data_ptr() if lse is not None else None,
-                               ws.data_ptr() if ws is not None else None, ws_bytes, _stream(dev))
-    check("li_attn_fwd_dense", st)
+    dtype_code(q)
+    lse = _run(ops.attn_dense, q, k, v, kt, vt, int(txt_len), float(sm_scale), out, bool(return_lse), bool(split))
     return (out, lse) if return_lse else out

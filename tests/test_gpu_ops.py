@@ -1,0 +1,89 @@
+"""GPU: the torch.ops.li operators pass torch.library.opcheck and trace under torch.compile.
+
+opcheck runs each operator for real on the GPU and checks its schema
+(mutated arguments are the annotated ones), its fake implementation against
+the real outputs, and its behaviour under AOT dispatch with dynamic shapes.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from li_sparse._ops import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _tokens(dev, B=1, H=2, frames=2, hw=(16, 16), scale=1.0, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    L = frames * hw[0] * hw[1]
+    return (torch.randn(B, L, H, 128, generator=g) * scale).to(torch.bfloat16).to(dev).permute(0, 2, 1, 3)
+
+
+def _lists(dev, H, nq, nk, kmax, seed=1):
+    rng = np.random.default_rng(seed)
+    ind = np.zeros((1, H, nq, kmax), np.int32)
+    cnt = np.zeros((1, H, nq), np.int32)
+    for h in range(H):
+        for r in range(nq):
+            n = int(rng.integers(1, kmax + 1))
+            ind[0, h, r, :n] = np.sort(rng.choice(nk, n, replace=False))
+            cnt[0, h, r] = n
+    return torch.from_numpy(ind).to(dev), torch.from_numpy(cnt).to(dev)
+
+
+def test_opcheck_attention_ops(dev):
+    print("[gpu] opcheck bsa_fwd_gather / bsa_fwd / attn_dense", flush=True)
+    q, k, v = _tokens(dev, scale=0.3, seed=1), _tokens(dev, frames=4, seed=2), _tokens(dev, frames=4, seed=3)
+    gq, gk = [2, 16, 16, 2, 8, 8, 2, 2], [4, 16, 16, 2, 8, 8, 2, 2]
+    ind, cnt = _lists(dev, 2, 4, 8, 5)
+    scale = 1.0 / math.sqrt(128)
+    torch.library.opcheck(ops.bsa_fwd_gather.default,
+                          (q, k, v, None, None, 0, gq, gk, ind, cnt, scale, torch.empty_like(q), True, True, False))
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    torch.library.opcheck(ops.bsa_fwd.default,
+                          (qc, kc, vc, ind, cnt, scale, 128, torch.empty_like(qc), True, True, False))
+    torch.library.opcheck(ops.attn_dense.default, (q, k, v, None, None, 0, scale, torch.empty_like(q), True, True))
+
+
+def test_opcheck_prep_and_mask_ops(dev):
+    print("[gpu] opcheck pool_pair / q_prep / kv_prep / untile / block_mask", flush=True)
+    q, k = _tokens(dev, seed=4), _tokens(dev, frames=4, seed=5)
+    gq, gk = [2, 16, 16, 2, 8, 8, 2, 2], [4, 16, 16, 2, 8, 8, 2, 2]
+    qp = torch.empty((1, 2, 4, 128), dtype=torch.bfloat16, device=dev)
+    kp = torch.empty((1, 2, 8, 128), dtype=torch.bfloat16, device=dev)
+    torch.library.opcheck(ops.pool_pair.default, (q, qp, 0, gq, k, kp, 0, gk))
+    qt = torch.empty((1, 2, 4, 128, 128), dtype=torch.bfloat16, device=dev)
+    torch.library.opcheck(ops.q_prep.default, (q, qt, qp, gq))
+    kt, vt = (torch.empty((1, 2, 8, 128, 128), dtype=torch.bfloat16, device=dev) for _ in range(2))
+    torch.library.opcheck(ops.kv_prep.default, (k, k, kt, vt, kp, 0, 0, gk))
+    torch.library.opcheck(ops.untile.default, (qt, torch.empty_like(q), gq))
+    # opcheck runs the ops above on copies, so qp / kp still hold whatever the allocator gave: fill them.
+    g = torch.Generator().manual_seed(9)
+    qp.copy_(torch.randn(qp.shape, generator=g).to(qp.dtype))
+    kp.copy_(torch.randn(kp.shape, generator=g).to(kp.dtype))
+    torch.library.opcheck(ops.block_mask.default,
+                          (qp, kp, 1, 0, 0.5, 7, 0, True, True, False, 2, 2, 0, 8, None, True))
+
+
+def test_compiled_graph_calls_the_ops(dev):
+    """torch.compile(fullgraph=True) traces the pools, the mask and the fused attention through their fakes."""
+    print("[gpu] torch.compile fullgraph over torch.ops.li", flush=True)
+    q, k, v = _tokens(dev, scale=0.3, seed=6), _tokens(dev, frames=4, seed=7), _tokens(dev, frames=4, seed=8)
+    gq, gk = [2, 16, 16, 2, 8, 8, 2, 2], [4, 16, 16, 2, 8, 8, 2, 2]
+
+    def call(q, k, v):
+        qp = q.new_empty((1, 2, 4, 128))
+        kp = q.new_empty((1, 2, 8, 128))
+        torch.ops.li.pool_pair(q, qp, 0, gq, k, kp, 0, gk)
+        ind, cnt, _ = torch.ops.li.block_mask(qp, kp, 1, 0, 0.5, 7, 0, True, True, False, 2, 2, 0, 8, None, False)
+        out = torch.empty_like(q)
+        torch.ops.li.bsa_fwd_gather(q, k, v, None, None, 0, gq, gk, ind, cnt, 1.0 / math.sqrt(128), out, False,
+                                    True, False)
+        return out
+
+    eager = call(q, k, v)
+    compiled = torch.compile(call, fullgraph=True, backend="aot_eager")(q, k, v)
+    torch.cuda.synchronize()
+    assert torch.equal(eager.view(torch.int16), compiled.view(torch.int16))
