@@ -52,17 +52,26 @@ struct BsaArgs {
   float* lse;
   int32_t NH, Lq, nkb, nqt, n_cols;
   float qk_scale;
-  // Tail split (D = 128, BS = 128 kernel only): work units u < n_full are
-  // whole query tiles; unit n_full + 2p + half is half `half` of tile
-  // n_full + p (the first or second half of its kept-block list), which
-  // writes unnormalised fp32 O and (m, l) rows to `part` for the merge kernel.
-  int32_t n_full;
+  // Query tiles of the launch (B * NH * nqt), placed on the XCDs by unit_tile.
+  int32_t ntiles;
+  // Tail split (D = 128, BS = 128 kernel only; ntiles a multiple of 8): XCD x
+  // (unit ids x, x + 8, ...) owns the xtiles = ntiles / 8 tiles from
+  // x * xtiles on.  When xsplit > 0, the last xsplit of them run as two
+  // halves of their kept-block list, the first ceil(count / 2) blocks and
+  // the rest.  Slot s of XCD x (unit 8 s + x) runs whole tile x * xtiles + s
+  // for s < xtiles - xsplit, then come the first halves of the split tiles,
+  // then their second halves, so a split tile's halves stay on the XCD whose
+  // L2 holds its head's keys.  Half e of split tile j of XCD x writes
+  // unnormalised fp32 O and (m, l) rows to partial slot 2 (x * xsplit + j) +
+  // e of `part` for the merge kernel.
+  int32_t xtiles, xsplit;
   float* part;
-  // Optional dispatch order of the whole tiles (a permutation of
-  // [0, n_full)): position p of the XCD-aware unit order runs tile order[p].
+  // Optional dispatch order of the tiles (a permutation of [0, ntiles);
+  // never with the tail split): position p of the XCD-aware unit order runs
+  // tile order[p].
   const int32_t* order;
   // XCD chunk: 0 gives each XCD one contiguous range of positions; C > 0
-  // (n_full a multiple of 8 C) deals chunks of C positions round-robin over
+  // (ntiles a multiple of 8 C) deals chunks of C positions round-robin over
   // the XCDs, so the tiles in flight at once span about 8 C positions.
   int32_t xchunk;
   // e4m3 kernel only: q and k hold e4m3 codes (1 byte per element) with one
@@ -73,7 +82,7 @@ struct BsaArgs {
   BsaGather g;
 };
 
-// Whole tile of work unit `id` (< a.n_full): ids are dealt round-robin over
+// Tile of work unit `id` (< a.ntiles): ids are dealt round-robin over
 // the 8 XCDs, so they are remapped to give each XCD a contiguous range of
 // positions; a.order, when given, names the tile at each position.
 __device__ __forceinline__ int unit_tile(const BsaArgs& a, int id) {
@@ -83,12 +92,12 @@ __device__ __forceinline__ int unit_tile(const BsaArgs& a, int id) {
     const int c = a.xchunk;
     pos = ((slot / c) * 8 + xcd) * c + slot % c;
   } else {
-    const int per = a.n_full >> 3, rem = a.n_full & 7;
+    const int per = a.ntiles >> 3, rem = a.ntiles & 7;
     pos = xcd * per + (xcd < rem ? xcd : rem) + slot;
   }
   if (!a.order) return pos;
   const int t = __builtin_amdgcn_readfirstlane(a.order[pos]);
-  return t < 0 ? 0 : (t >= a.n_full ? a.n_full - 1 : t);
+  return t < 0 ? 0 : (t >= a.ntiles ? a.ntiles - 1 : t);
 }
 
 namespace {

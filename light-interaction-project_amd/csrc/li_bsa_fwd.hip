@@ -452,18 +452,21 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   const int qq = wave >> 1, kh = wave & 1;
   const int l32 = lane & 31, hl = lane >> 5;
 
-  // Work unit -> query tile.  Ids below n_full are whole tiles, remapped so
-  // that each XCD (ids are dealt round-robin over the 8 XCDs) takes a
-  // contiguous range of them.  The split half-units come last in dispatch
-  // order and keep their natural order, so they spread evenly over the XCDs;
-  // unit n_full + 2p + half is half `half` of tile n_full + p.
+  // Work unit -> query tile: unit_tile gives each XCD (ids are dealt
+  // round-robin over the 8 XCDs) a contiguous range of tiles; with the tail
+  // split, the last slots of an XCD run the halves of its split tiles
+  // (`half` = which half, `pslot` = its partial slot).
   const int id = blockIdx.x;
-  int tile, half = -1;
-  if (id < a.n_full) {
+  int tile, half = -1, pslot = 0;
+  if (a.xsplit == 0 || (id >> 3) < a.xtiles - a.xsplit) {
     tile = unit_tile(a, id);
   } else {
-    tile = a.n_full + ((id - a.n_full) >> 1);
-    half = (id - a.n_full) & 1;
+    const int x = id & 7;
+    int j = (id >> 3) - (a.xtiles - a.xsplit);
+    half = j >= a.xsplit ? 1 : 0;
+    j -= half ? a.xsplit : 0;
+    tile = x * a.xtiles + (a.xtiles - a.xsplit) + j;
+    pslot = 2 * (x * a.xsplit + j) + half;
   }
   const int bh = tile / a.nqt, m = tile % a.nqt;
   const int b = bh / a.NH, h = bh % a.NH;
@@ -487,7 +490,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   }
   const int row0 = m * BS;
   // Partial rows of a split unit: O as [128 rows][128 d] fp32, then (m, l).
-  float* part_o = half >= 0 ? a.part + (int64_t)(2 * (tile - a.n_full) + half) * BS * (D + 2) : nullptr;
+  float* part_o = half >= 0 ? a.part + (int64_t)pslot * BS * (D + 2) : nullptr;
   float* part_ml = half >= 0 ? part_o + BS * D : nullptr;
 
   // Output row of tile row rt, or null when it is not stored (past Lq, or
@@ -1181,12 +1184,14 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
 // Combines the two halves of each split query tile: O = (O0 a0 + O1 a1) /
 // (l0 a0 + l1 a1) with a_i = 2^(m_i - max(m0, m1)); lse = max + log2(l).  Four
 // workgroups per split tile (32 rows each), eight threads per row (16 d each,
-// 64 contiguous bytes of each partial).
+// 64 contiguous bytes of each partial).  Split tile p = x * xsplit + j is
+// tile j of the split tiles of XCD x.
 template <typename E, bool G = false>
 __global__ __launch_bounds__(256) void bsa_merge_kernel(BsaArgs a) {
   constexpr int BS = 128, D = 128;
   const int p = blockIdx.x >> 2;
-  const int tile = a.n_full + p;
+  const int x = p / a.xsplit, j = p - x * a.xsplit;
+  const int tile = x * a.xtiles + (a.xtiles - a.xsplit) + j;
   const int bh = tile / a.nqt, m = tile % a.nqt;
   const int rt = (blockIdx.x & 3) * 32 + (threadIdx.x >> 3), dq = threadIdx.x & 7;
   const int r = m * BS + rt;
@@ -1235,9 +1240,9 @@ __global__ __launch_bounds__(256) void bsa_merge_kernel(BsaArgs a) {
 
 template <typename E, bool DN = false>
 int launch_bsa_gather(BsaArgs& a, int tiles, hipStream_t s) {
-  const int nsplit = tiles - a.n_full;
+  const int nsplit = 8 * a.xsplit;
   clear_launch_error();
-  hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, 128, true, false, DN>), dim3(a.n_full + 2 * nsplit),
+  hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, 128, true, false, DN>), dim3(tiles + nsplit),
                      dim3(DmaCfg<128>::NTHR), 0, s, a);
   if (nsplit > 0) hipLaunchKernelGGL((bsa_merge_kernel<E, true>), dim3(4 * nsplit), dim3(256), 0, s, a);
   return launch_status();
@@ -1245,9 +1250,9 @@ int launch_bsa_gather(BsaArgs& a, int tiles, hipStream_t s) {
 
 template <bool G>
 int launch_bsa_fp8(BsaArgs& a, int tiles, hipStream_t s) {
-  const int nsplit = tiles - a.n_full;
+  const int nsplit = 8 * a.xsplit;
   clear_launch_error();
-  hipLaunchKernelGGL((bsa_fwd_dma_kernel<Bf16, 128, G, true>), dim3(a.n_full + 2 * nsplit), dim3(DmaCfg<128>::NTHR),
+  hipLaunchKernelGGL((bsa_fwd_dma_kernel<Bf16, 128, G, true>), dim3(tiles + nsplit), dim3(DmaCfg<128>::NTHR),
                      0, s, a);
   if (nsplit > 0) hipLaunchKernelGGL((bsa_merge_kernel<Bf16, G>), dim3(4 * nsplit), dim3(256), 0, s, a);
   return launch_status();
@@ -1255,9 +1260,9 @@ int launch_bsa_fp8(BsaArgs& a, int tiles, hipStream_t s) {
 
 template <typename E, int BS>
 int launch_bsa_dma(BsaArgs& a, int tiles, hipStream_t s) {
-  const int nsplit = tiles - a.n_full;
+  const int nsplit = 8 * a.xsplit;
   clear_launch_error();
-  hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, BS>), dim3(a.n_full + 2 * nsplit), dim3(DmaCfg<BS>::NTHR), 0, s, a);
+  hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, BS>), dim3(tiles + nsplit), dim3(DmaCfg<BS>::NTHR), 0, s, a);
   if constexpr (BS == 128) {
     if (nsplit > 0) hipLaunchKernelGGL(bsa_merge_kernel<E>, dim3(4 * nsplit), dim3(256), 0, s, a);
   }
@@ -1305,7 +1310,7 @@ int device_cus() {
 __global__ __launch_bounds__(1024) void bsa_order_kernel(BsaArgs a, int32_t* order) {
   __shared__ int hist[1024];
   const int tid = threadIdx.x, x = blockIdx.x;
-  const int tiles = a.n_full;
+  const int tiles = a.ntiles;
   const int per = tiles >> 3, rem = tiles & 7;
   int start = x * per + (x < rem ? x : rem), len = per + (x < rem ? 1 : 0);
   if (a.xchunk > 0) {
@@ -1343,14 +1348,23 @@ __global__ __launch_bounds__(1024) void bsa_order_kernel(BsaArgs a, int32_t* ord
   }
 }
 
-// Query tiles whose block lists are split in two.  With one 8-wave
-// workgroup per CU, `tiles` whole tiles take ceil(tiles / cus) rounds; when
-// the last round holds r <= cus/2 tiles, splitting those r tiles into 2r half
-// units makes that round half as long.
-int64_t split_tiles(int64_t tiles, int cus) {
-  if (cus <= 0 || tiles <= cus) return 0;
-  const int64_t r = tiles % cus;
-  return (r > 0 && 2 * r <= cus) ? r : 0;
+// Query tiles of each XCD whose block lists are split in halves.  The tiles
+// are dealt to the 8 XCDs in contiguous ranges of n = tiles / 8, and with
+// one 8-wave workgroup per CU an XCD of c = cus / 8 CUs runs its n tiles in
+// ceil(n / c) rounds, the last holding r = n % c tiles.  When r <= c / 2,
+// those r tiles run as 2 r halves on their own XCD (so that their key blocks
+// stay in its L2), and the last round is half as long (HY shape: 896 tiles,
+// n = 112, c = 32, r = 16).  A fuller last round is left whole: at the
+// Matrix-Game shape (n = 90, r = 26) uneven pieces (5/6 of a list on 26 CUs,
+// the 1/6 pieces on the other 6) ran as long as the whole round, each short
+// piece paying ~4 us of prologue and epilogue, and the merge added ~10 us.
+// No split when the tiles or the CUs do not divide evenly over the XCDs.
+int64_t split_per_xcd(int64_t tiles, int cus) {
+  if (cus <= 0 || cus % 8 != 0 || tiles % 8 != 0) return 0;
+  const int64_t n = tiles / 8, c = cus / 8;
+  if (n <= c) return 0;
+  const int64_t r = n % c;
+  return 2 * r <= c ? r : 0;
 }
 
 constexpr int64_t kPartBytesPerTile = 2 * 128 * (128 + 2) * 4;
@@ -1365,13 +1379,15 @@ int64_t order_bytes(int64_t tiles) { return (tiles * 4 + 15) & ~(int64_t)15; }
 // each XCD sorts and runs one head at a time and its L2 holds that head's
 // K/V blocks (HY long rollout: 0.687 against 0.706 ms with two heads mixed per
 // XCD).  0 when the heads do not split evenly over the XCDs.
-int xcd_chunk(int64_t n_full, int32_t nqt) {
-  return (nqt > 0 && n_full > 0 && n_full % (8 * (int64_t)nqt) == 0) ? nqt : 0;
+int xcd_chunk(int64_t tiles, int32_t nqt) {
+  return (nqt > 0 && tiles > 0 && tiles % (8 * (int64_t)nqt) == 0) ? nqt : 0;
 }
 
 int plan_units(BsaArgs& a, int64_t tiles, int32_t D, int32_t block_size, void* workspace, int64_t workspace_bytes,
                int32_t flags, hipStream_t s) {
-  a.n_full = (int32_t)tiles;
+  a.ntiles = (int32_t)tiles;
+  a.xtiles = (int32_t)(tiles / 8);
+  a.xsplit = 0;
   a.part = nullptr;
   a.order = nullptr;
   if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0 || D != 128) return LI_OK;
@@ -1387,9 +1403,9 @@ int plan_units(BsaArgs& a, int64_t tiles, int32_t D, int32_t block_size, void* w
     return st;
   }
   if (block_size != 128) return LI_OK;
-  const int64_t ns = split_tiles(tiles, device_cus());
-  if (ns > 0 && workspace_bytes >= ns * kPartBytesPerTile) {
-    a.n_full = (int32_t)(tiles - ns);
+  const int64_t r = split_per_xcd(tiles, device_cus());
+  if (r > 0 && workspace_bytes >= 8 * r * kPartBytesPerTile) {
+    a.xsplit = (int32_t)r;
     a.part = static_cast<float*>(workspace);
   }
   return LI_OK;
@@ -1403,7 +1419,7 @@ using namespace li;
 extern "C" int64_t li_bsa_fwd_workspace_size(int32_t B, int32_t NH, int32_t Lq, int32_t D, int32_t block_size) {
   if (B <= 0 || NH <= 0 || Lq <= 0 || D != 128 || block_size <= 0) return 0;
   const int64_t tiles = (int64_t)((Lq + block_size - 1) / block_size) * B * NH;
-  const int64_t split = block_size == 128 ? split_tiles(tiles, device_cus()) * kPartBytesPerTile : 0;
+  const int64_t split = block_size == 128 ? 8 * split_per_xcd(tiles, device_cus()) * kPartBytesPerTile : 0;
   const int64_t ord = order_bytes(tiles);
   return split > ord ? split : ord;
 }

@@ -89,29 +89,43 @@ def test_full_hy_shape_sampled_tiles(dev):
     assert err <= TOL
 
 
-def test_tail_split_matches_whole_tiles_and_oracle(dev):
-    """Tiles of a partial last round run as two halves of their block list plus a merge kernel."""
+def split_per_xcd(tiles, cus):
+    """Tail-split tiles per XCD, restated from the rule the library documents: n = tiles / 8 tiles per XCD
+    on c = cus / 8 CUs; its last round's r = n % c tiles are split in halves when r <= c / 2."""
+    if cus % 8 or tiles % 8:
+        return 0
+    n, c = tiles // 8, cus // 8
+    r = n % c if n > c else 0
+    return r if 2 * r <= c else 0
+
+
+@pytest.mark.parametrize("H,nq", [(8, 44), (8, 58)])
+def test_tail_split_matches_whole_tiles_and_oracle(dev, H, nq):
+    """Each XCD's tiles of a partial last round run as two halves of their block list plus a merge kernel
+    when the round is at most half full (8 x 44 tiles on 256 CUs: 12 of each XCD's 44); a fuller last round
+    (8 x 58: 26 of 58) runs whole.  Both against whole tiles and the oracle."""
     from li_sparse import _lib
 
-    bs, D, B, H, nq, nkb = 128, 128, 1, 3, 100, 12
+    bs, D, B, nkb = 128, 128, 1, 12
     Lq, Lk = nq * bs - 40, nkb * bs
     print(f"[gpu] bsa tail split B={B} H={H} Lq={Lq} Lk={Lk}", flush=True)
     tiles = B * H * nq
     with torch.cuda.device(dev):
         ws = _lib.lib.li_bsa_fwd_workspace_size(B, H, Lq, D, bs)
         cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    r = tiles % cus if tiles > cus else 0
-    nsplit = r if 0 < r <= cus // 2 else 0
+    r = split_per_xcd(tiles, cus)
+    nsplit = 8 * r
+    print(f"[gpu]   {r} split tiles per XCD", flush=True)
     # room for the split partials, or for the tile order of the balanced mode
     assert ws == max(nsplit * 2 * 128 * 130 * 4, (tiles * 4 + 15) // 16 * 16)
     rng = np.random.default_rng(5)
     q, k, v = _inputs(41, B, H, Lq, Lk, D)
     ind, cnt = _random_lists(rng, B, H, nq, nkb, 7)
-    # empty, single-block and two-block lists among the split tiles (the last `nsplit` tiles)
+    # empty, single-block and two-block lists among the split tiles (the last r tiles of each XCD's range)
     flat = cnt.reshape(-1)
     for j, n in enumerate([0, 1, 2, 0, 1]):
-        if nsplit > j:
-            flat[tiles - 1 - 3 * j] = n
+        if r > 0:
+            flat[(j % 8 + 1) * (tiles // 8) - 1 - (j // 8) % r] = n
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     ii, cc = torch.from_numpy(ind).to(dev), torch.from_numpy(cnt).to(dev)
     scale = 1.0 / math.sqrt(D)

@@ -154,7 +154,7 @@ def test_fp8_attention_random_lists_vs_oracle(dev):
 
 def test_fp8_split_and_balance(dev):
     """Tail split within fp32 rounding of whole tiles; the balanced order gives the same bits as whole tiles."""
-    B, H, nq, nkb, bs, D = 1, 3, 100, 12, 128, 128
+    B, H, nq, nkb, bs, D = 1, 8, 44, 12, 128, 128  # 352 tiles: 12 of each XCD's 44 split on 256 CUs
     Lq, Lk = nq * bs - 40, nkb * bs
     print(f"[gpu] fp8 bsa split/balance B={B} H={H} Lq={Lq} Lk={Lk}", flush=True)
     x = _quantized_inputs(9, B, H, Lq, Lk, D)
