@@ -104,6 +104,32 @@ def wall_loop(fn, iters, stream=None):
     return (t2 - t0) * 1e3 / iters, (t1 - t0) * 1e3 / iters, gpu
 
 
+def interleaved(fns, iters, stream):
+    """Times the functions in ``fns`` alternately, ``iters`` rounds of one call each, with events on ``stream``.
+
+    Returns the per-call GPU ms of each function.  Alternating puts every
+    function in the same clock and power state, which back-to-back loops
+    measured minutes apart do not (the MI355X clock dips for some tens of
+    calls after a heavy load starts, then settles).
+    """
+    import torch
+
+    per = [[] for _ in fns]
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in fns]
+          for _ in range(iters)]
+    torch.cuda.synchronize()
+    for i in range(iters):
+        for j, fn in enumerate(fns):
+            ev[i][j][0].record(stream)
+            fn()
+            ev[i][j][1].record(stream)
+    torch.cuda.synchronize()
+    for i in range(iters):
+        for j in range(len(fns)):
+            per[j].append(ev[i][j][0].elapsed_time(ev[i][j][1]))
+    return per
+
+
 def mean(xs):
     return sum(xs) / len(xs)
 
@@ -316,6 +342,18 @@ def main():
                       "own_dense_kernel_tflops": round(dense_flops / (own_ms * 1e-3) / 1e12, 2),
                       "speedup_call_vs_own_dense": round(own_ms / step_ms, 3),
                       "speedup_attention_vs_own_dense": round(own_ms / attn_ms, 3)})
+        # The call, its attention kernel and the dense kernel alternated call by
+        # call, so that all three see the same clock state.
+        c_per, a_per, d_per = interleaved([step, attn, own], args.steps, stream)
+        c_ms, a_ms, d_ms = mean(c_per), mean(a_per), mean(d_per)
+        dense["interleaved"] = {
+            "call_ms": round(c_ms, 4), "attention_ms": round(a_ms, 4), "own_dense_kernel_ms": round(d_ms, 4),
+            "speedup_call_vs_own_dense": round(d_ms / c_ms, 3),
+            "speedup_attention_vs_own_dense": round(d_ms / a_ms, 3),
+            "note": "the call, its attention kernel and the dense kernel timed alternately, one call each per "
+                    "round for --steps rounds (events on the launch stream), so the three ratios share one "
+                    "clock state; speedup_call_vs_own_dense above divides a steady-state dense time by the "
+                    "headline loop's wall time, which right after the warm-up runs in the GPU's clock dip"}
     if args.compare_dense:
         all_ind = torch.arange(g.nk_blk, dtype=torch.int32, device=dev).expand(B, H, g.nq_blk, g.nk_blk).contiguous()
         all_cnt = torch.full((B, H, g.nq_blk), g.nk_blk, dtype=torch.int32, device=dev)
