@@ -46,6 +46,9 @@ CASES = [
     ("mg_tile_4x4x8", 1, 2, (22, 40), (4, 4, 8), 4, 8, 0, "blhd", torch.bfloat16),
     ("odd_frames_edge", 1, 2, (12, 20), (2, 8, 8), 3, 7, 130, "blhd", torch.bfloat16),
     ("hy_small_f16_text", 1, 2, (30, 52), (2, 8, 8), 2, 6, 200, "blhd", torch.float16),
+    # full HY shape with 200 text tokens: 896 tiles, so 16 of each XCD's 112 run as split halves, the first half
+    # holding the text blocks
+    ("hy_full_text_split", 1, 16, (30, 52), (2, 8, 8), 4, 12, 200, "blhd", torch.bfloat16),
 ]
 
 
