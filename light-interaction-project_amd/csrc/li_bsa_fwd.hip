@@ -1015,18 +1015,17 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       sk_n = ksc[safe(id_n)];
       sk_nn = ksc[safe(id_nn)];
     }
+    // The prologue waits only for K(0) (with the Q fragments); group 0 issues
+    // the loads of V(0) and K(1) at the head of its S(0) and waits for them
+    // at the end of its X(0), so they land while S(0) and X(0) run.
+    Blk vb0{nullptr, nullptr, 0u}, kb1{nullptr, nullptr, 0u};
     if (grp == 0) {
       const Geo g0 = geo_of(safe(id_c)), g1 = geo_of(safe(id_n));
-      const Blk vb0 = blk_src(g0, true);
+      vb0 = blk_src(g0, true);
       const Blk kb0 = blk_src(g0, false);
-      const Blk kb1 = blk_src(g1, false);
+      kb1 = blk_src(g1, false);
 #pragma unroll
-      for (int n = 0; n < LPW; ++n) dma(n, vb0, kb0, a_vs0, a_ks1);
-#pragma unroll
-      for (int n = 0; n < KPW; ++n) {
-        dma(n + LPW, vb0, kb0, a_vs0, a_ks1);
-        dma(n + LPW, vb0, kb1, a_vs0, a_ks0);
-      }
+      for (int n = 0; n < KPW; ++n) dma(n + LPW, vb0, kb0, a_vs0, a_ks1);
       geo_k = geo_of(safe(id_nn));
       dv = blk_src(g1, true);
       dk = blk_src(geo_k, false);
@@ -1066,10 +1065,17 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       if (load) wait_loads();
     };
     auto run = [&](bool load) LI_INLINE {
+      if (load) {
+#pragma unroll
+        for (int n = 0; n < LPW; ++n) dma(n, vb0, kb1, a_vs0, a_ks0);
+#pragma unroll
+        for (int n = 0; n < KPW; ++n) dma(n + LPW, vb0, kb1, a_vs0, a_ks0);
+      }
       scores(ks1);
       if (!load) barrier();
       if constexpr (F8) qk_scale = qk_base * ksc[safe(id_c)];
       x_phase(id_c, [] {});
+      if (load) wait_loads();
       if (!load) {
         for (int i = 0; i < count; i += 2) {
           pair(i, vs0, ks0, a_vs1, a_ks1, false);
