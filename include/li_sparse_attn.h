@@ -190,13 +190,23 @@ int li_block_mask(int dtype, int32_t B, int32_t NH, int32_t D,
  * smaller than required) every tile runs whole.  Results are the same up to
  * fp32 rounding of the combination.
  *
- * flags: 0, or LI_BSA_BALANCE for rows of unequal length (ragged budgets):
- * with the workspace, a small kernel first sorts the query tiles by their
- * kept-block counts and the tiles start longest first (no tail split then).
- * It changes the order of work only; results are identical to flags = 0
- * without a tail split.  Used by the D = 128 kernels; ignored for D = 64.
+ * flags: a combination of
+ *  LI_BSA_BALANCE for rows of unequal length (ragged budgets): with the
+ *    workspace, a small kernel first sorts the query tiles by their
+ *    kept-block counts and the tiles start longest first (no tail split
+ *    then).  It changes the order of work only; results are identical to
+ *    flags = 0 without a tail split.  Used by the D = 128 kernels; ignored
+ *    for D = 64.
+ *  LI_BSA_SORTED (token-order entry points only, li_bsa_fwd_gather and its
+ *    variants; ignored here): every row lists its text blocks (ids below
+ *    num_txt_blk) before its visual blocks, as the mask builder's ascending
+ *    lists do.  The kernel then reads the out-of-grid chunks of visual
+ *    blocks from a zero region at the visual chunks' own offsets, which
+ *    saves a vector select per load; same results, bit for bit.  A text
+ *    block listed after a visual block reads as zeros under this flag.
+ *    No counterpart in the reference (its lists are always ascending).
  */
-enum li_bsa_flags { LI_BSA_BALANCE = 1 };
+enum li_bsa_flags { LI_BSA_BALANCE = 1, LI_BSA_SORTED = 2 };
 int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int32_t D,
                const void* q, const void* k, const void* v,
                const int32_t* block_indices, const int64_t idx_strides[4], int32_t n_cols,

@@ -80,6 +80,14 @@ struct BsaArgs {
   const float* k_scale;
   // Fused path only (kernel template flag); unused otherwise.
   BsaGather g;
+  // Zero-region kernels (fused path, rows listing their text blocks first):
+  // zero bytes reaching past the largest K / V row offset of a tile from its
+  // origin token.  An out-of-grid chunk of a visual block is read from here
+  // at the visual chunk's own lane offsets, so a load picks only its scalar
+  // base.  The first gen_pairs block phases of a tile (an even count, enough
+  // to cover the text blocks' loads) pick base and lane offset per chunk.
+  const char* zero_region;
+  int32_t gen_pairs;
 };
 
 // Tile of work unit `id` (< a.ntiles): ids are dealt round-robin over
@@ -185,6 +193,18 @@ __device__ __forceinline__ DmaSrc dma_sel(uint32_t mask, int bit, const void* sa
       : [base] "=&s"(r.base), [lm] "=&s"(lm), [voff] "=&v"(r.voff)
       : [mask] "s"(mask), [bit] "i"(bit), [sa] "s"(sa), [sb] "s"(sb), [va] "v"(va), [vb] "v"(vb)
       : "scc");
+  return r;
+}
+// The base sa when bit `bit` of the wave-uniform `mask` is set, else sb,
+// with one lane offset for both (two scalar instructions).
+__device__ __forceinline__ DmaSrc dma_sel_base(uint32_t mask, int bit, const void* sa, const void* sb, uint32_t voff) {
+  DmaSrc r;
+  asm("s_bitcmp1_b32 %[mask], %[bit]\n\t"
+      "s_cselect_b64 %[base], %[sa], %[sb]"
+      : [base] "=&s"(r.base)
+      : [mask] "s"(mask), [bit] "i"(bit), [sa] "s"(sa), [sb] "s"(sb)
+      : "scc");
+  r.voff = voff;
   return r;
 }
 __device__ __forceinline__ void wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }

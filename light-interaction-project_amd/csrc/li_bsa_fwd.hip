@@ -428,7 +428,8 @@ __device__ __forceinline__ void sched_m_phase() {
 // DN (dense calls, token-order addressing only): no index lists, every tile
 // keeps blocks 0 .. n_cols - 1; queries and keys past the token bounds are
 // skipped, and the padding rows of the last text and visual blocks score -inf.
-template <typename E, int BS, bool G = false, bool F8 = false, bool DN = false>
+// ZR (with G): the zero-region load path (BsaArgs::zero_region, gen_pairs).
+template <typename E, int BS, bool G = false, bool F8 = false, bool DN = false, bool ZR = false>
 __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   using C = DmaCfg<BS>;
   static_assert(!G || BS == 128, "token-order addressing is built for 128-row tiles");
@@ -879,7 +880,11 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     };
     // Chunk n of a group-0 wave's share of a stage: n < LPW is V, else K.
     // src_n gives its global source, issue_n loads it into the stage.
-    auto src_n = [&](int n, const Blk& sv, const Blk& sk) LI_INLINE {
+    // zr = Stage<1>: the zero-region source (visual or zero base, visual lane
+    // offset); text blocks, whose mask is 0, then read as zeros, so these
+    // phases come after a row's text blocks.  Stage<0>: base and lane offset
+    // per chunk (visual, text or the small zero buffer).
+    auto src_n = [&](int n, const Blk& sv, const Blk& sk, auto zr) LI_INLINE {
       const bool isv = n < LPW;
       const int j = isv ? n : n - LPW;
       const Blk& s_ = isv ? sv : sk;
@@ -887,6 +892,8 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       const char* alt = j < 4 ? s_.alt : s_.alt + 4096;
       if (!G || (F8 && !isv))
         return DmaSrc{alt, lin};
+      else if constexpr (decltype(zr)::value == 1)
+        return dma_sel_base(s_.mask, j, s_.vis, a.zero_region, isv ? vvo[j] : kvo[j]);
       else
         return dma_sel(s_.mask, j, s_.vis, isv ? vvo[j] : kvo[j], alt, lin);
     };
@@ -898,7 +905,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       dma16_imm(src.base, src.voff, (isv ? vn + c * 1024 : kn + c * (F8 ? 1024 : 1088)) - imm, imm);
     };
     auto dma = [&](int n, const Blk& sv, const Blk& sk, uint32_t vn, uint32_t kn) LI_INLINE {
-      issue_n(n, src_n(n, sv, sk), vn, kn);
+      issue_n(n, src_n(n, sv, sk, Stage<0>{}), vn, kn);
     };
     // A operand of MFMA u of an M phase: the V^T tile of P V step
     // (st, dt) = (u / NDT, u % NDT) for u < NPV, else the K tile of S step
@@ -945,7 +952,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     // vb / kb: load sources of the V and K blocks the phase fetches, worked
     // out during the preceding softmax phase.
     auto m_phase = [&](const char* vc, const char* kc, uint32_t vn, uint32_t kn, const Blk& vb, const Blk& kb,
-                       bool load) LI_INLINE {
+                       bool load, auto zr) LI_INLINE {
       Op opb[LA];
 #pragma unroll
       for (int u = 0; u < LA; ++u) opb[u] = read_op(u, vc, kc);
@@ -953,7 +960,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       // between the MFMAs.  The NL loads are spread evenly: load n follows
       // MFMA u when floor(u NL / NU) = n < floor((u + 1) NL / NU).
       DmaSrc nxt{nullptr, 0u};
-      if (load) nxt = src_n(0, vb, kb);
+      if (load) nxt = src_n(0, vb, kb, zr);
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
         const Op op = opb[u % LA];
@@ -962,7 +969,7 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
         const int n = u * NL / NU;
         if (load && (u + 1) * NL / NU > n) {
           issue_n(n, nxt, vn, kn);
-          if (n + 1 < NL) nxt = src_n(n + 1, vb, kb);
+          if (n + 1 < NL) nxt = src_n(n + 1, vb, kb, zr);
         }
       }
       sched_m_phase<NPV, F8 ? 2 : 1, NU, LA>();
@@ -1035,9 +1042,10 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     // Each group runs its own copy of the block loop (group 0's with the
     // stage loads), so neither carries the other's load code and the copies
     // meet only after the loop.
-    auto pair = [&](int i, const char* vc, const char* kc, uint32_t vn, uint32_t kn, bool load) LI_INLINE {
+    auto pair = [&](int i, const char* vc, const char* kc, uint32_t vn, uint32_t kn, bool load,
+                    auto zr) LI_INLINE {
       barrier();
-      m_phase(vc, kc, vn, kn, dv, dk, load);
+      m_phase(vc, kc, vn, kn, dv, dk, load, zr);
       barrier();
       const int id_x = id_n;
       id_c = id_n;
@@ -1078,23 +1086,38 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       if (load) wait_loads();
       if (!load) {
         for (int i = 0; i < count; i += 2) {
-          pair(i, vs0, ks0, a_vs1, a_ks1, false);
-          if (i + 1 < count) pair(i + 1, vs1, ks1, a_vs0, a_ks0, false);
+          pair(i, vs0, ks0, a_vs1, a_ks1, false, Stage<0>{});
+          if (i + 1 < count) pair(i + 1, vs1, ks1, a_vs0, a_ks0, false, Stage<0>{});
         }
       } else {
         // The last block's phase loads nothing, since its V(i + 1) and
         // K(i + 2) lie past the row: a separate copy of that phase skips the
-        // loads and the wait for them (one memory round trip per tile).
+        // loads and the wait for them (one memory round trip per tile).  On
+        // the zero-region path the phases after the first gen_pairs load with
+        // the zero-region sources; the others (the row's text blocks, and the
+        // last loading phase, which may still reach a short row's text
+        // blocks) pick their sources per chunk.
         int i = 0;
-        for (; i + 2 < count; i += 2) {
-          pair(i, vs0, ks0, a_vs1, a_ks1, true);
-          pair(i + 1, vs1, ks1, a_vs0, a_ks0, true);
+        if constexpr (ZR) {
+          for (; i < a.gen_pairs && i + 2 < count; i += 2) {
+            pair(i, vs0, ks0, a_vs1, a_ks1, true, Stage<0>{});
+            pair(i + 1, vs1, ks1, a_vs0, a_ks0, true, Stage<0>{});
+          }
+          for (; i + 2 < count; i += 2) {
+            pair(i, vs0, ks0, a_vs1, a_ks1, true, Stage<1>{});
+            pair(i + 1, vs1, ks1, a_vs0, a_ks0, true, Stage<1>{});
+          }
+        } else {
+          for (; i + 2 < count; i += 2) {
+            pair(i, vs0, ks0, a_vs1, a_ks1, true, Stage<0>{});
+            pair(i + 1, vs1, ks1, a_vs0, a_ks0, true, Stage<0>{});
+          }
         }
         if (i + 1 < count) {
-          pair(i, vs0, ks0, a_vs1, a_ks1, true);
-          pair(i + 1, vs1, ks1, a_vs0, a_ks0, false);
+          pair(i, vs0, ks0, a_vs1, a_ks1, true, Stage<0>{});
+          pair(i + 1, vs1, ks1, a_vs0, a_ks0, false, Stage<0>{});
         } else {
-          pair(i, vs0, ks0, a_vs1, a_ks1, false);
+          pair(i, vs0, ks0, a_vs1, a_ks1, false, Stage<0>{});
         }
       }
       if (load) barrier();
@@ -1265,8 +1288,12 @@ template <typename E, bool DN = false>
 int launch_bsa_gather(BsaArgs& a, int tiles, hipStream_t s) {
   const int nsplit = 8 * a.xsplit;
   clear_launch_error();
-  hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, 128, true, false, DN>), dim3(tiles + nsplit),
-                     dim3(DmaCfg<128>::NTHR), 0, s, a);
+  if (a.zero_region)
+    hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, 128, true, false, DN, true>), dim3(tiles + nsplit),
+                       dim3(DmaCfg<128>::NTHR), 0, s, a);
+  else
+    hipLaunchKernelGGL((bsa_fwd_dma_kernel<E, 128, true, false, DN>), dim3(tiles + nsplit),
+                       dim3(DmaCfg<128>::NTHR), 0, s, a);
   if (nsplit > 0) hipLaunchKernelGGL((bsa_merge_kernel<E, true>), dim3(4 * nsplit), dim3(256), 0, s, a);
   return launch_status();
 }
@@ -1275,8 +1302,12 @@ template <bool G>
 int launch_bsa_fp8(BsaArgs& a, int tiles, hipStream_t s) {
   const int nsplit = 8 * a.xsplit;
   clear_launch_error();
-  hipLaunchKernelGGL((bsa_fwd_dma_kernel<Bf16, 128, G, true>), dim3(tiles + nsplit), dim3(DmaCfg<128>::NTHR),
-                     0, s, a);
+  if (G && a.zero_region)
+    hipLaunchKernelGGL((bsa_fwd_dma_kernel<Bf16, 128, G, true, false, G>), dim3(tiles + nsplit),
+                       dim3(DmaCfg<128>::NTHR), 0, s, a);
+  else
+    hipLaunchKernelGGL((bsa_fwd_dma_kernel<Bf16, 128, G, true>), dim3(tiles + nsplit), dim3(DmaCfg<128>::NTHR),
+                       0, s, a);
   if (nsplit > 0) hipLaunchKernelGGL((bsa_merge_kernel<Bf16, G>), dim3(4 * nsplit), dim3(256), 0, s, a);
   return launch_status();
 }
@@ -1490,13 +1521,51 @@ extern "C" int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t 
 
 namespace {
 
-
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // (B, NH, L, D) view usable by the fused kernel: unit d stride, 16-byte rows.
 bool row_view_ok(const void* p, const int64_t st[4]) {
   return p && aligned16(p) && st[3] == 1 && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 && st[2] > 0;
 }
+
+}  // namespace
+
+// Zero bytes for the zero-region kernels (BsaArgs::zero_region): a static
+// array, zero from module load and never written.  Each device holds its own
+// copy until the process ends; host code passes zero_region_ptr(), never the
+// array's name.
+constexpr int64_t kZeroRegionBytes = 64ll << 20;
+static __device__ __align__(256) char g_zero_region[kZeroRegionBytes];
+
+namespace {
+
+// Device address of g_zero_region on the current device (looked up once per
+// device), or null, in which case the kernels pick their sources per chunk.
+const char* zero_region_ptr() {
+  static std::mutex mu;
+  static void* ptrs[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_zero_region)) != hipSuccess) return nullptr;
+    ptrs[dev] = p;
+  }
+  return static_cast<const char*>(ptrs[dev]);
+}
+
+// Zero-region set-up of a fused call whose K / V rows lie up to max_row
+// tokens of st elements from their tile's origin token (plus one 128-element
+// row), with ntxt text blocks at the head of every row: the region when it
+// reaches that far, else null; and the leading block phases that still pick
+// their sources per chunk (those whose loads can reach a text block, rounded
+// up to an even count).
+void setup_zero_region(BsaArgs& a, int64_t max_row, int64_t st, int32_t ntxt) {
+  a.zero_region = (max_row * st + 128) * 2 <= kZeroRegionBytes ? zero_region_ptr() : nullptr;
+  a.gen_pairs = ((ntxt > 1 ? ntxt - 1 : 0) + 1) & ~1;
+}
+
 
 // Checks and BsaArgs of a token-order (fused) call over the q_geom / k_geom
 // grids.  With e4m3 keys (k8) only V is read in token order: k / k_strides
@@ -1508,7 +1577,7 @@ int gather_setup(BsaArgs& a, int64_t& tiles, int32_t B, int32_t NH, int32_t D, c
                  const li_tile_geom* q_geom, const li_tile_geom* k_geom, const int32_t* block_indices,
                  const int64_t idx_strides[4], int32_t n_cols, const int32_t* block_counts,
                  const int64_t cnt_strides[3], float sm_scale, void* out, const int64_t out_strides[4], float* lse,
-                 bool k8) {
+                 bool k8, bool sorted) {
   tiles = 0;
   if (!v_strides || !out_strides || !q_geom || !k_geom || !block_indices || !idx_strides || !block_counts ||
       !cnt_strides || (!k8 && (!q_strides || !k_strides)))
@@ -1544,6 +1613,7 @@ int gather_setup(BsaArgs& a, int64_t& tiles, int32_t B, int32_t NH, int32_t D, c
   const int64_t max_row = (int64_t)(gq.tt - 1) * gq.H * gq.W + (int64_t)(gq.th - 1) * gq.W + gq.tw - 1;
   const int64_t kv_st = !k8 && k_strides[2] > v_strides[2] ? k_strides[2] : v_strides[2];
   if ((max_row * kv_st + D) * 2 > (1ll << 32)) return LI_ERR_SHAPE;
+  if (sorted) setup_zero_region(a, max_row, kv_st, num_txt_blk);
   if (nq == 0) return LI_OK;
   tiles = nq * B * NH;
   if (tiles > 0x7FFFFFFF) return LI_ERR_SHAPE;
@@ -1609,7 +1679,7 @@ extern "C" int li_bsa_fwd_gather(int dtype, int32_t B, int32_t NH, int32_t D, co
   int64_t tiles = 0;
   int st = gather_setup(a, tiles, B, NH, D, q, q_strides, k, k_strides, v, v_strides, k_txt, v_txt, num_txt_blk,
                         q_geom, k_geom, block_indices, idx_strides, n_cols, block_counts, cnt_strides, sm_scale, out,
-                        out_strides, lse, false);
+                        out_strides, lse, false, (flags & LI_BSA_SORTED) != 0);
   if (st != LI_OK || tiles == 0) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
   st = plan_units(a, tiles, D, 128, workspace, workspace_bytes, flags, s);
@@ -1664,7 +1734,7 @@ extern "C" int li_bsa_fwd_gather_noalloc(int dtype, int32_t B, int32_t NH, int32
   int64_t tiles = 0;
   int st = gather_setup(a, tiles, B, NH, D, q, q_strides, k, k_strides, v, v_strides, k_txt, v_txt, num_txt_blk,
                         q_geom, k_geom, block_indices, idx_strides, n_cols, block_counts, cnt_strides, sm_scale, out,
-                        out_strides, lse, false);
+                        out_strides, lse, false, (flags & LI_BSA_SORTED) != 0);
   if (st != LI_OK || tiles == 0) return st;
   // The workspace li_bsa_fwd_gather would use for this call must fit the scratch.
   const int64_t need = li_bsa_fwd_workspace_size(B, NH, a.nqt * 128, D, 128);
@@ -1738,7 +1808,7 @@ extern "C" int li_bsa_fwd_fp8_gather(int32_t B, int32_t NH, int32_t D, const voi
   int64_t tiles = 0;
   int st = gather_setup(a, tiles, B, NH, D, q8, nullptr, k8, nullptr, v, v_strides, nullptr, v_txt, num_txt_blk,
                         q_geom, k_geom, block_indices, idx_strides, n_cols, block_counts, cnt_strides, sm_scale, out,
-                        out_strides, lse, true);
+                        out_strides, lse, true, (flags & LI_BSA_SORTED) != 0);
   if (st != LI_OK || tiles == 0) return st;
   a.q_scale = q_scale;
   a.k_scale = k_scale;
@@ -1772,6 +1842,8 @@ extern "C" int li_attn_fwd_dense(int dtype, int32_t B, int32_t NH, int32_t D, in
   const int64_t tiles = nq * B * NH;
   if (tiles > 0x7FFFFFFF) return LI_ERR_SHAPE;
   BsaArgs a = {};
+  // Every tile keeps blocks 0 .. n - 1 in order, text blocks first.
+  setup_zero_region(a, 127, kv_st, (int32_t)ntxt);
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
   a.v = static_cast<const uint16_t*>(v);

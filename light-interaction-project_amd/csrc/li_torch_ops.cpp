@@ -248,7 +248,7 @@ at::Tensor bsa_fwd_gather(const at::Tensor& q, const at::Tensor& k, const at::Te
                           const c10::optional<at::Tensor>& k_txt, const c10::optional<at::Tensor>& v_txt,
                           int64_t num_txt_blk, c10::IntArrayRef q_geom, c10::IntArrayRef k_geom,
                           const at::Tensor& indices, const at::Tensor& counts, double sm_scale, at::Tensor& out,
-                          bool return_lse, bool split, bool balance) {
+                          bool return_lse, bool split, bool balance, bool sorted) {
   gpu(q, "q");
   rank(q, 4, "q");
   rank(k, 4, "k");
@@ -275,7 +275,7 @@ at::Tensor bsa_fwd_gather(const at::Tensor& q, const at::Tensor& k, const at::Te
       v.data_ptr(), vs.data(), ptr(kt), ptr(vt), (int32_t)num_txt_blk, &gq, &gk, indices.data_ptr<int32_t>(),
       is.data(), (int32_t)indices.size(3), counts.data_ptr<int32_t>(), cs.data(), (float)sm_scale, out.data_ptr(),
       os.data(), return_lse ? lse.data_ptr<float>() : nullptr, ptr(ws), ws.defined() ? ws.numel() * 4 : 0,
-      balance ? LI_BSA_BALANCE : 0, stream_of(q));
+      (balance ? LI_BSA_BALANCE : 0) | (sorted ? LI_BSA_SORTED : 0), stream_of(q));
   check("li_bsa_fwd_gather", st);
   return lse;
 }
@@ -385,7 +385,7 @@ at::Tensor bsa_fwd_fp8_gather(const at::Tensor& q8, const at::Tensor& q_scale, c
                               const at::Tensor& k_scale, const at::Tensor& v, const c10::optional<at::Tensor>& v_txt,
                               int64_t num_txt_blk, c10::IntArrayRef q_geom, c10::IntArrayRef k_geom,
                               const at::Tensor& indices, const at::Tensor& counts, double sm_scale, at::Tensor& out,
-                              bool return_lse, bool balance) {
+                              bool return_lse, bool balance, bool sorted) {
   gpu(q8, "q8");
   rank(v, 4, "v");
   rank(out, 4, "out");
@@ -406,7 +406,8 @@ at::Tensor bsa_fwd_fp8_gather(const at::Tensor& q8, const at::Tensor& q_scale, c
       k_scale.data_ptr<float>(), v.data_ptr(), vs.data(), ptr(vt), (int32_t)num_txt_blk, &gq, &gk,
       indices.data_ptr<int32_t>(), is.data(), (int32_t)indices.size(3), counts.data_ptr<int32_t>(), cs.data(),
       (float)sm_scale, out.data_ptr(), os.data(), return_lse ? lse.data_ptr<float>() : nullptr, ptr(ws),
-      ws.defined() ? ws.numel() * 4 : 0, balance ? LI_BSA_BALANCE : 0, stream_of(v));
+      ws.defined() ? ws.numel() * 4 : 0, (balance ? LI_BSA_BALANCE : 0) | (sorted ? LI_BSA_SORTED : 0),
+      stream_of(v));
   check("li_bsa_fwd_fp8_gather", st);
   return lse;
 }
@@ -428,7 +429,7 @@ TORCH_LIBRARY(li, m) {
         "Tensor(a!) out, bool return_lse, bool split, bool balance) -> Tensor");
   m.def("bsa_fwd_gather(Tensor q, Tensor k, Tensor v, Tensor? k_txt, Tensor? v_txt, int num_txt_blk, int[] q_geom, "
         "int[] k_geom, Tensor indices, Tensor counts, float sm_scale, Tensor(a!) out, bool return_lse, bool split, "
-        "bool balance) -> Tensor");
+        "bool balance, bool sorted=False) -> Tensor");
   m.def("attn_dense(Tensor q, Tensor k, Tensor v, Tensor? k_txt, Tensor? v_txt, int txt_len, float sm_scale, "
         "Tensor(a!) out, bool return_lse, bool split) -> Tensor");
   m.def("tile_prep_fp8(Tensor src, Tensor(a!) dst, Tensor(b!) scales, Tensor(c!)? mean, int dst_off, int pool_off, "
@@ -439,7 +440,7 @@ TORCH_LIBRARY(li, m) {
         "float sm_scale, int block_size, Tensor(a!) out, bool return_lse, bool split, bool balance) -> Tensor");
   m.def("bsa_fwd_fp8_gather(Tensor q8, Tensor q_scale, Tensor k8, Tensor k_scale, Tensor v, Tensor? v_txt, "
         "int num_txt_blk, int[] q_geom, int[] k_geom, Tensor indices, Tensor counts, float sm_scale, "
-        "Tensor(a!) out, bool return_lse, bool balance) -> Tensor");
+        "Tensor(a!) out, bool return_lse, bool balance, bool sorted=False) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(li, CUDA, m) {

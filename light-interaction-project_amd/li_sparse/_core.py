@@ -204,12 +204,14 @@ def fused_supported(D, tile, latent_hw):
 
 
 def bsa_forward_gather(q, k, v, k_txt, v_txt, num_txt_blk, T_q, T_k, H, W, tt, th, tw, nh, nw, indices, counts,
-                       sm_scale, out, return_lse=False, split=True, balance=False):
+                       sm_scale, out, return_lse=False, split=True, balance=False, sorted_lists=False):
     """Block-sparse attention reading Q/K/V in token order and writing ``out`` in token order (li_bsa_fwd_gather).
 
     q/out (B,NH,Lq,D) and k/v (B,NH,Lk,D) views with any strides the kernel accepts; k_txt/v_txt the
     zero-padded (B,NH,num_txt_blk*BS,D) contiguous text keys/values or None.  ``split`` and ``balance``
-    as for ``bsa_forward``.  No host sync.
+    as for ``bsa_forward``.  ``sorted_lists`` (LI_BSA_SORTED): every row lists its text blocks before its
+    visual blocks, as the block mask's ascending lists do, which lets the kernel take its faster load path
+    (same results; a text block listed after a visual block would read as zeros).  No host sync.
     """
     _device_check(q, k, v, out, indices, counts)
     _same_dtype(q, k, v, out)
@@ -231,7 +233,7 @@ def bsa_forward_gather(q, k, v, k_txt, v_txt, num_txt_blk, T_q, T_k, H, W, tt, t
     lse = _run(ops.bsa_fwd_gather, q, k, v, k_txt if num_txt_blk > 0 else None,
                v_txt if num_txt_blk > 0 else None, int(num_txt_blk), [T_q, H, W, tt, th, tw, nh, nw],
                [T_k, H, W, tt, th, tw, nh, nw], indices, counts, float(sm_scale), out, bool(return_lse), bool(split),
-               bool(balance))
+               bool(balance), bool(sorted_lists))
     return (out, lse) if return_lse else out
 
 
@@ -458,12 +460,12 @@ def bsa_forward_fp8(q8, q_scale, k8, k_scale, v, indices, counts, sm_scale, bloc
 
 
 def bsa_forward_fp8_gather(q8, q_scale, k8, k_scale, v, v_txt, num_txt_blk, T_q, T_k, H, W, tt, th, tw, nh, nw,
-                           indices, counts, sm_scale, out, return_lse=False, balance=False):
+                           indices, counts, sm_scale, out, return_lse=False, balance=False, sorted_lists=False):
     """e4m3 attention with V read and O written in token order (see li_bsa_fwd_fp8_gather).
 
     q8 (B,NH,nq_blk*128,D) / k8 (B,NH,(num_txt_blk+nk_blk)*128,D) e4m3 tiles with their (B,NH,nblk) scales;
     v (B,NH,Lk,D) bf16 token view; v_txt (B,NH,num_txt_blk*128,D) contiguous zero-padded or None;
-    out (B,NH,Lq,D) bf16 token view, written at valid tokens.
+    out (B,NH,Lq,D) bf16 token view, written at valid tokens.  ``sorted_lists`` as for bsa_forward_gather.
     """
     _device_check(q8, q_scale, k8, k_scale, v, indices, counts, out)
     if q8.dtype != FP8 or k8.dtype != FP8 or v.dtype != torch.bfloat16 or out.dtype != torch.bfloat16:
@@ -484,7 +486,7 @@ def bsa_forward_fp8_gather(q8, q_scale, k8, k_scale, v, v_txt, num_txt_blk, T_q,
         raise ValueError("v_txt must be a contiguous (B, NH, num_txt_blk*128, D) buffer")
     lse = _run(ops.bsa_fwd_fp8_gather, q8, q_scale, k8, k_scale, v, v_txt if num_txt_blk > 0 else None,
                int(num_txt_blk), [T_q, H, W, tt, th, tw, nh, nw], [T_k, H, W, tt, th, tw, nh, nw], indices, counts,
-               float(sm_scale), out, bool(return_lse), bool(balance))
+               float(sm_scale), out, bool(return_lse), bool(balance), bool(sorted_lists))
     return (out, lse) if return_lse else out
 
 

@@ -16,7 +16,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL below)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libli_sparse_attn.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 LI_OK = 0
 LI_ERR_INVALID_ARG = -1
@@ -38,6 +38,7 @@ LI_BUDGET_HISTORY = 0
 LI_BUDGET_TOTAL = 1
 
 LI_BSA_BALANCE = 1
+LI_BSA_SORTED = 2
 
 _i64p = ctypes.POINTER(ctypes.c_int64)
 _i32p = ctypes.POINTER(ctypes.c_int32)

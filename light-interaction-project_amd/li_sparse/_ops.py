@@ -94,7 +94,7 @@ def _bsa_fwd_fake(q, k, v, indices, counts, sm_scale, block_size, out, return_ls
 
 @torch.library.register_fake("li::bsa_fwd_gather")
 def _bsa_fwd_gather_fake(q, k, v, k_txt, v_txt, num_txt_blk, q_geom, k_geom, indices, counts, sm_scale, out,
-                         return_lse, split, balance):
+                         return_lse, split, balance, sorted=False):
     B, NH = q.shape[:2]
     bs = q_geom[3] * q_geom[4] * q_geom[5]
     return _lse(q, return_lse, B, NH, _nblk(q_geom) * bs)
@@ -125,6 +125,6 @@ def _bsa_fwd_fp8_fake(q8, q_scale, k8, k_scale, v, indices, counts, sm_scale, bl
 
 @torch.library.register_fake("li::bsa_fwd_fp8_gather")
 def _bsa_fwd_fp8_gather_fake(q8, q_scale, k8, k_scale, v, v_txt, num_txt_blk, q_geom, k_geom, indices, counts,
-                             sm_scale, out, return_lse, balance):
+                             sm_scale, out, return_lse, balance, sorted=False):
     B, NH = v.shape[:2]
     return _lse(v, return_lse, B, NH, _nblk(q_geom) * 128)

@@ -207,7 +207,8 @@ def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events
     _stage(events, "index_end")
     _stage(events, "attn_start")
     _core.bsa_forward_gather(q, k_vis, v_vis, kb["kt"], kb["vt"], g.num_txt_blk, g.T_q, g.T_k, g.H, g.W, g.tt, g.th,
-                             g.tw, g.nh, g.nw, indices, counts, 1.0 / math.sqrt(D), o_out, balance=balance)
+                             g.tw, g.nh, g.nw, indices, counts, 1.0 / math.sqrt(D), o_out, balance=balance,
+                             sorted_lists=True)
     _stage(events, "attn_end")
     _stage(events, "untile_start")
     _stage(events, "untile_end")
@@ -272,7 +273,7 @@ def _fused_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, ev
     _stage(events, "attn_start")
     _core.bsa_forward_fp8_gather(q8.flatten(2, 3), q_scale, kb["k8"].flatten(2, 3), kb["k_scale"], v_vis, kb["vt"],
                                  g.num_txt_blk, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw, indices, counts,
-                                 1.0 / math.sqrt(D), o_out, balance=balance)
+                                 1.0 / math.sqrt(D), o_out, balance=balance, sorted_lists=True)
     _stage(events, "attn_end")
     _stage(events, "untile_start")
     _stage(events, "untile_end")
@@ -284,7 +285,9 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
     """One sparse-attention forward.
 
     q (B,H,Lq,D); k_txt/v_txt (B,H,N_txt,D) or None; k_vis/v_vis (B,H,Lk,D), any strides.
-    ``select(q_pool, k_pool, text_len, grid_q, grid_k) -> (indices, counts)``.
+    ``select(q_pool, k_pool, text_len, grid_q, grid_k) -> (indices, counts)``, with every row listing its
+    text blocks before its visual blocks, as the block mask's ascending lists do (the fused kernels take
+    their faster load path on that basis).
     ``events`` (dict or None) collects CUDA events per stage for profiling.
     ``fused`` (default) runs pools + one gather/attend/untile kernel where the
     shape allows it (D = 128, 128-token tiles, tw and W multiples of 4, a grid

@@ -76,6 +76,40 @@ def test_fused_equals_tiled(dev, case):
     assert same
 
 
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_sorted_lists_path_gives_the_same_bits(dev, case):
+    """LI_BSA_SORTED (the zero-region load path: text blocks first, out-of-grid chunks read from a zero region at
+    the visual offsets) against the per-chunk source selection on the mask's own ascending lists: same bits,
+    with text blocks, grids with partial tiles, the (4,4,8) tile, f16 and the tail split."""
+    name, B, H, hw, tile, fq, fk, text, layout, dtype = case
+    Hh, W = hw
+    D = 128
+    print(f"[gpu] sorted-lists path vs per-chunk selection {name}", flush=True)
+    q, k, v, kt, vt = _qkv(sum(map(ord, name)) + 1, B, H, fq * Hh * W, fk * Hh * W, D, layout, text, dtype)
+    q, k, v = q.to(dev), k.to(dev), v.to(dev)
+    g = _pipeline.geometry(hw, tile, q.shape[2], k.shape[2], text)
+    k_txt = v_txt = None
+    if text:
+        k_txt = torch.zeros((B, H, g.num_txt_blk * g.bs, D), dtype=dtype, device=dev)
+        v_txt = torch.zeros_like(k_txt)
+        k_txt[:, :, :text] = kt.to(dev)
+        v_txt[:, :, :text] = vt.to(dev)
+    q_pool = torch.empty((B, H, g.nq_blk, D), device=dev, dtype=dtype)
+    k_pool = torch.empty((B, H, g.nk_blk, D), device=dev, dtype=dtype)
+    _core.pool(q, q_pool, 0, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    _core.pool(k, k_pool, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
+    params = {"tile_size": tile, "topk_ratio": 0.3, "recent_protect": tile[0], "sim_metric": "scaled_dot_product",
+              "force_diag": True, "force_sink": True}
+    ind, cnt = fast_generate_indices(q_pool, k_pool, text, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), params, dev)
+    args = (q, k, v, k_txt, v_txt, g.num_txt_blk, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw, ind, cnt,
+            1.0 / math.sqrt(D))
+    out_s, lse_s = _core.bsa_forward_gather(*args, torch.empty_like(q), return_lse=True, sorted_lists=True)
+    out_u, lse_u = _core.bsa_forward_gather(*args, torch.empty_like(q), return_lse=True, sorted_lists=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out_s.view(torch.int16), out_u.view(torch.int16))
+    assert torch.equal(lse_s.view(torch.int32), lse_u.view(torch.int32))
+
+
 def test_fused_hy_shape_with_split_and_lse(dev):
     """Full HY decode shape (896 query tiles: the tail split runs) and the LSE of both paths."""
     B, H, D, hw, tile = 1, 16, 128, (30, 52), (2, 8, 8)
