@@ -276,7 +276,7 @@ def main():
     tiled_attn = lambda: _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs, balance=balance)  # noqa: E731
     fused_attn = lambda: _core.bsa_forward_gather(  # noqa: E731
         qd, kd, vd, None, None, 0, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw, ind, cnt, scale, o_tok,
-        balance=balance)
+        balance=balance, sorted_lists=True)
     # The roofline kernel is the attention kernel the call launches.
     attn = fused_attn if fused else tiled_attn
     if fp8:
@@ -291,7 +291,7 @@ def main():
                                                   balance=balance)
         fused_fp8 = lambda: _core.bsa_forward_fp8_gather(  # noqa: E731
             q8f, qs, k8f, ks, vd, None, 0, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw, ind, cnt, scale,
-            o_tok, balance=balance)
+            o_tok, balance=balance, sorted_lists=True)
         attn = fused_fp8 if fused else tiled_fp8
 
     if args.profile:
@@ -365,9 +365,9 @@ def main():
         dense["own_kernel_all_blocks_ms"] = round(full_ms, 4)
         dense["own_kernel_all_blocks_tflops"] = round(full_flops / (full_ms * 1e-3) / 1e12, 2)
     if fp8:
-        kname = "bsa_fwd_dma_kernel<bf16,128,gather,e4m3>" if fused else "bsa_fwd_dma_kernel<bf16,128,e4m3>"
+        kname = "bsa_fwd_dma_kernel<bf16,128,gather,e4m3,zero-region>" if fused else "bsa_fwd_dma_kernel<bf16,128,e4m3>"
     elif fused:
-        kname = "bsa_fwd_dma_kernel<bf16,128,gather>"
+        kname = "bsa_fwd_dma_kernel<bf16,128,gather,zero-region>"
     elif D == 128 and bs in (64, 128):
         kname = "bsa_fwd_dma_kernel<bf16,128>"
     else:
@@ -482,7 +482,8 @@ def profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params
             _core.tile_prep_fp8(kd, k8, ks, k_pool, 0, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
             fast_generate_indices(q_pool, k_pool, 0, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), params, dev)
             _core.bsa_forward_fp8_gather(q8.flatten(2, 3), qs, k8.flatten(2, 3), ks, vd, None, 0, g.T_q, g.T_k, g.H,
-                                         g.W, g.tt, g.th, g.tw, g.nh, g.nw, ind, cnt, scale, o_tok, balance=balance)
+                                         g.W, g.tt, g.th, g.tw, g.nh, g.nw, ind, cnt, scale, o_tok, balance=balance,
+                                         sorted_lists=True)
             _core.kv_prep_fp8(kd, vd, k8, ks, v_all, k_pool, 0, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
             _core.bsa_forward_fp8(q8.flatten(2, 3), qs, k8.flatten(2, 3), ks, vf, ind, cnt, scale, bs, out=out,
                                   balance=balance)
@@ -495,7 +496,7 @@ def profile_kernels(args, wl, g, qd, kd, vd, q_t, q_p, k_all, v_all, k_p, params
             _core.pool(kd, k_pool, 0, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
             fast_generate_indices(q_pool, k_pool, 0, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), params, dev)
             _core.bsa_forward_gather(qd, kd, vd, None, None, 0, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh,
-                                     g.nw, ind, cnt, scale, o_tok, balance=balance)
+                                     g.nw, ind, cnt, scale, o_tok, balance=balance, sorted_lists=True)
             _core.bsa_forward(qf, kf, vf, ind, cnt, scale, bs, out=out, balance=balance)
         else:
             _core.q_prep(qd, q_t, q_p, g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
