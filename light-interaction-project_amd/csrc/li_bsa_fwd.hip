@@ -477,8 +477,65 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   uint16_t* ohead = a.out + (int64_t)bh * a.Lq * D;
   constexpr int KEB = F8 ? 1 : 2;  // bytes per K element
   const char* kbytes = reinterpret_cast<const char*>(a.k) + (int64_t)bh * a.nkb * BS * D * KEB;
+  const int row0 = m * BS;
+
+  // Q^T fragments first: their loads depend on the tile alone, so they go
+  // out together with the loads of the count and the first block ids below.
+  // Lanes without a query row read row 0 of the head and keep zeros, which
+  // keeps the loads free of branches.
+  vec8 qf[C::DS];
+  // e4m3 Q^T fragments: lane holds query row l32 and bytes 64 s + 32 hl .. +31.
+  i32x8 qf8[2];
+  float qk_scale = a.qk_scale;
+  if constexpr (F8) {
+    const int r = row0 + 32 * qq + l32;
+    const bool ok = r < a.Lq;
+    const char* qrow8 = reinterpret_cast<const char*>(a.q) + ((int64_t)bh * a.Lq + (ok ? r : 0)) * D;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      u32x4 lo = *reinterpret_cast<const u32x4*>(qrow8 + 64 * s + 32 * hl);
+      u32x4 hi = *reinterpret_cast<const u32x4*>(qrow8 + 64 * s + 32 * hl + 16);
+      if (!ok) lo = hi = u32x4{0u, 0u, 0u, 0u};
+      qf8[s] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    }
+    typedef __attribute__((address_space(4))) const float const_f32;
+    qk_scale *= ((const_f32*)a.q_scale)[(int64_t)bh * a.nqt + m];
+  } else {
+    const uint16_t* qrow;
+    bool ok;
+    if constexpr (G) {
+      const int32_t l = tile_token(a.g, a.g.Tq, m, 32 * qq + l32, ok);
+      ok = ok && (!DN || l < a.g.q_tokens);
+      qrow = a.q + b * a.g.qs[0] + h * a.g.qs[1] + (int64_t)(ok ? l : 0) * a.g.qs[2];
+    } else {
+      const int r = row0 + 32 * qq + l32;
+      ok = r < a.Lq;
+      qrow = qhead + (int64_t)(ok ? r : 0) * D;
+    }
+#pragma unroll
+    for (int s = 0; s < C::DS; ++s) {
+      u32x4 x = *reinterpret_cast<const u32x4*>(qrow + 16 * s + 8 * hl);
+      if (!ok) x = u32x4{0u, 0u, 0u, 0u};
+      qf[s] = __builtin_bit_cast(vec8, x);
+    }
+  }
+
   // Dense calls: tile m keeps blocks 0 .. n_cols - 1, ids id_base + i.
+  typedef __attribute__((address_space(4))) const int32_t const_i32;
   const int32_t* irow = DN ? nullptr : a.idx + b * a.is[0] + h * a.is[1] + (int64_t)m * a.is[2];
+  // The first four entries of the row (clamped to its columns), read through
+  // the scalar cache without waiting for the count, which picks among them;
+  // the second half of a split tile reads its own after the count.
+  int r0 = -1, r1 = -1, r2 = -1, r3 = -1;
+  auto read_first = [&](const int32_t* row, int ncols) LI_INLINE {
+    const const_i32* rs = (const const_i32*)row;
+    const int64_t is3 = a.is[3];
+    r0 = rs[0];
+    r1 = rs[(int64_t)(1 < ncols ? 1 : ncols - 1) * is3];
+    r2 = rs[(int64_t)(2 < ncols ? 2 : ncols - 1) * is3];
+    r3 = rs[(int64_t)(3 < ncols ? 3 : ncols - 1) * is3];
+  };
+  if (!DN && half != 1 && a.n_cols > 0) read_first(irow, a.n_cols);
   int count = DN ? a.n_cols : a.cnt[b * a.cs[0] + h * a.cs[1] + (int64_t)m * a.cs[2]];
   count = count < 0 ? 0 : (count > a.n_cols ? a.n_cols : count);
   count = __builtin_amdgcn_readfirstlane(count);
@@ -488,8 +545,14 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     if constexpr (!DN) irow += half ? (int64_t)h0 * a.is[3] : 0;
     id_base = half ? h0 : 0;
     count = half ? count - h0 : h0;
+    if (!DN && half == 1 && a.n_cols - h0 > 0) read_first(irow, a.n_cols - h0);
   }
-  const int row0 = m * BS;
+  // An empty list (or an empty half of a split tile) runs as one block with
+  // an out-of-range id, which gets all-zero probabilities: the epilogue then
+  // writes zero rows and an LSE of -inf (zero partials and (m, l) = (-inf, 0)
+  // for a half), with no early exit to hold back the loads above.
+  const bool empty = count == 0;
+  count = empty ? 1 : count;
   // Partial rows of a split unit: O as [128 rows][128 d] fp32, then (m, l).
   float* part_o = half >= 0 ? a.part + (int64_t)pslot * BS * (D + 2) : nullptr;
   float* part_ml = half >= 0 ? part_o + BS * D : nullptr;
@@ -506,62 +569,6 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       return row0 + rt < a.Lq ? ohead + (int64_t)(row0 + rt) * D : nullptr;
     }
   };
-
-  if (count == 0) {
-    if (half >= 0) {
-      for (int u = tid; u < BS * D / 4; u += C::NTHR)
-        reinterpret_cast<f32x4*>(part_o)[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      for (int r = tid; r < BS; r += C::NTHR) {
-        part_ml[2 * r] = -__builtin_inff();
-        part_ml[2 * r + 1] = 0.0f;
-      }
-      return;
-    }
-    for (int u = tid; u < BS * (D / 8); u += C::NTHR) {
-      uint16_t* orow = out_row(u / (D / 8));
-      if (orow) *reinterpret_cast<u32x4*>(orow + 8 * (u % (D / 8))) = u32x4{0u, 0u, 0u, 0u};
-    }
-    if (a.lse)
-      for (int r = tid; r < BS; r += C::NTHR)
-        if (row0 + r < a.Lq) a.lse[(int64_t)bh * a.Lq + row0 + r] = -__builtin_inff();
-    return;
-  }
-
-  vec8 qf[C::DS];
-  // e4m3 Q^T fragments: lane holds query row l32 and bytes 64 s + 32 hl .. +31.
-  i32x8 qf8[2];
-  float qk_scale = a.qk_scale;
-  if constexpr (F8) {
-    const int r = row0 + 32 * qq + l32;
-    const char* qrow8 = reinterpret_cast<const char*>(a.q) + ((int64_t)bh * a.Lq + r) * D;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
-      if (r < a.Lq) {
-        lo = *reinterpret_cast<const u32x4*>(qrow8 + 64 * s + 32 * hl);
-        hi = *reinterpret_cast<const u32x4*>(qrow8 + 64 * s + 32 * hl + 16);
-      }
-      qf8[s] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-    }
-    typedef __attribute__((address_space(4))) const float const_f32;
-    qk_scale *= ((const_f32*)a.q_scale)[(int64_t)bh * a.nqt + m];
-  } else {
-    const uint16_t* qrow = nullptr;
-    if constexpr (G) {
-      bool ok;
-      const int32_t l = tile_token(a.g, a.g.Tq, m, 32 * qq + l32, ok);
-      if (ok && (!DN || l < a.g.q_tokens)) qrow = a.q + b * a.g.qs[0] + h * a.g.qs[1] + (int64_t)l * a.g.qs[2];
-    } else {
-      const int r = row0 + 32 * qq + l32;
-      if (r < a.Lq) qrow = qhead + (int64_t)r * D;
-    }
-#pragma unroll
-    for (int s = 0; s < C::DS; ++s) {
-      u32x4 x = {0u, 0u, 0u, 0u};
-      if (qrow) x = *reinterpret_cast<const u32x4*>(qrow + 16 * s + 8 * hl);
-      qf[s] = __builtin_bit_cast(vec8, x);
-    }
-  }
 
   // DMA source byte offsets of this lane within a chunk; the chunk base is
   // wave-uniform (scalar registers), so each load is base + constant lane
@@ -712,14 +719,13 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
   };
 
   // Block ids are wave-uniform: read them through the scalar cache.
-  typedef __attribute__((address_space(4))) const int32_t const_i32;
   const_i32* irow_s = (const_i32*)irow;
   auto block_id = [&](int i) LI_INLINE {
     const int j = i < count ? i : count - 1;
     if constexpr (DN)
-      return id_base + j;
+      return empty ? -1 : id_base + j;
     else
-      return (int)irow_s[(int64_t)j * a.is[3]];
+      return empty ? -1 : (int)irow_s[(int64_t)j * a.is[3]];
   };
   auto valid = [&](int id_) LI_INLINE { return (unsigned)id_ < (unsigned)a.nkb; };
   auto safe = [&](int id_) LI_INLINE { return valid(id_) ? id_ : 0; };
@@ -1006,7 +1012,15 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     };
     // Block ids i+1 .. i+3 are kept ahead of block i, so the sources of the
     // next M phase can be worked out before it starts.
-    int id_c = block_id(0), id_n = block_id(1), id_nn = block_id(2), id_n3 = block_id(3);
+    int id_c, id_n, id_nn, id_n3;
+    if constexpr (DN) {
+      id_c = block_id(0), id_n = block_id(1), id_nn = block_id(2), id_n3 = block_id(3);
+    } else {
+      id_c = empty ? -1 : r0;
+      id_n = count > 1 ? r1 : id_c;
+      id_nn = count > 2 ? r2 : id_n;
+      id_n3 = count > 3 ? r3 : id_nn;
+    }
     // The next id to read, stepped along the row and held at its last entry
     // (the same clamp as block_id), so a read costs no index arithmetic.
     const int64_t ist = a.is[3];
