@@ -179,7 +179,8 @@ int li_block_mask(int dtype, int32_t B, int32_t NH, int32_t D,
  * Out-of-range ids add nothing and access nothing out of bounds (callers
  * validate beforehand): the D=64 kernel skips them; the D=128 kernel fetches
  * block 0 in their place and gives it zero probability (the same result when
- * block 0 holds finite values).
+ * block 0 holds finite values).  Lk = 0 (no key block at all) is
+ * LI_ERR_SHAPE, here and on every attention entry point below.
  * Built for block_size in {64, 128} and D in {64, 128}.
  *
  * workspace (optional, device, 16-byte aligned, NULL allowed): scratch of

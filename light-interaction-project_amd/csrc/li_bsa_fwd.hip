@@ -536,7 +536,8 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     r3 = rs[(int64_t)(3 < ncols ? 3 : ncols - 1) * is3];
   };
   if (!DN && half != 1 && a.n_cols > 0) read_first(irow, a.n_cols);
-  int count = DN ? a.n_cols : a.cnt[b * a.cs[0] + h * a.cs[1] + (int64_t)m * a.cs[2]];
+  const int32_t* cnt_at = DN ? nullptr : a.cnt + b * a.cs[0] + h * a.cs[1] + (int64_t)m * a.cs[2];
+  int count = DN ? a.n_cols : *cnt_at;
   count = count < 0 ? 0 : (count > a.n_cols ? a.n_cols : count);
   count = __builtin_amdgcn_readfirstlane(count);
   int id_base = 0;
@@ -1024,7 +1025,12 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     // The next id to read, stepped along the row and held at its last entry
     // (the same clamp as block_id), so a read costs no index arithmetic.
     const int64_t ist = a.is[3];
-    const_i32* idp = DN ? nullptr : irow_s + (int64_t)(count > 4 ? 4 : (count > 0 ? count - 1 : 0)) * ist;
+    // An empty unit's row may have no entry to read (no columns, or the
+    // second half of a one-block list): its pointer is the count it was
+    // given, which is readable, and the value read is never used.
+    const_i32* idp = DN ? nullptr
+                        : empty ? (const_i32*)cnt_at
+                                : irow_s + (int64_t)(count > 4 ? 4 : (count > 0 ? count - 1 : 0)) * ist;
     Blk dv{nullptr, nullptr, 0u}, dk{nullptr, nullptr, 0u};
     Geo geo_k{0, 0, 0u, false};  // geometry of the K block of the next M phase
     // F8: K scales of blocks id_n and id_nn, read one pair ahead of their
@@ -1523,6 +1529,9 @@ extern "C" int li_bsa_fwd(int dtype, int32_t B, int32_t NH, int32_t Lq, int32_t 
   a.NH = NH;
   a.Lq = Lq;
   a.nkb = Lk / block_size;
+  // No key block at all: there is nothing to attend to (and no block 0 to
+  // stand in for out-of-range ids).
+  if (a.nkb <= 0) return LI_ERR_SHAPE;
   a.nqt = (int32_t)nqt;
   a.n_cols = n_cols;
   a.qk_scale = sm_scale * 1.44269504f;
@@ -1643,6 +1652,7 @@ int gather_setup(BsaArgs& a, int64_t& tiles, int32_t B, int32_t NH, int32_t D, c
   a.NH = NH;
   a.Lq = (int32_t)(nq * 128);
   a.nkb = (int32_t)(nkv + num_txt_blk);
+  if (a.nkb <= 0) return LI_ERR_SHAPE;  // no key block at all
   a.nqt = (int32_t)nq;
   a.n_cols = n_cols;
   a.qk_scale = sm_scale * 1.44269504f;
@@ -1798,6 +1808,9 @@ extern "C" int li_bsa_fwd_fp8(int32_t B, int32_t NH, int32_t Lq, int32_t Lk, int
   a.NH = NH;
   a.Lq = Lq;
   a.nkb = Lk / block_size;
+  // No key block at all: there is nothing to attend to (and no block 0 to
+  // stand in for out-of-range ids).
+  if (a.nkb <= 0) return LI_ERR_SHAPE;
   a.nqt = (int32_t)nqt;
   a.n_cols = n_cols;
   a.qk_scale = sm_scale * 1.44269504f;
@@ -1868,6 +1881,7 @@ extern "C" int li_attn_fwd_dense(int dtype, int32_t B, int32_t NH, int32_t D, in
   a.NH = NH;
   a.Lq = (int32_t)(nq * 128);
   a.nkb = (int32_t)(ntxt + nvis);
+  if (a.nkb <= 0) return LI_ERR_SHAPE;  // no key block at all
   a.nqt = (int32_t)nq;
   a.n_cols = a.nkb;
   a.qk_scale = sm_scale * 1.44269504f;

@@ -40,6 +40,10 @@ def test_host_validation_needs_no_gpu():
     bsa = L.lib.li_bsa_fwd
     # K length not a multiple of the block size
     assert bsa(0, 1, 1, 128, 200, 128, fake, fake, fake, fake, s4, 1, fake, s3, 1.0, 128, fake, None, None, 0, 0, None) == L.LI_ERR_K_LEN
+    # no key block at all (Lk = 0), on the bf16 and the e4m3 tiled entry points
+    assert bsa(0, 1, 1, 128, 0, 128, fake, fake, fake, fake, s4, 1, fake, s3, 1.0, 128, fake, None, None, 0, 0, None) == L.LI_ERR_SHAPE
+    assert L.lib.li_bsa_fwd_fp8(1, 1, 128, 0, 128, fake, fake, fake, fake, fake, fake, s4, 1, fake, s3, 1.0, 128, fake,
+                                None, None, 0, 0, None) == L.LI_ERR_SHAPE
     # null pointers
     assert bsa(0, 1, 1, 128, 256, 128, None, fake, fake, fake, s4, 1, fake, s3, 1.0, 128, fake, None, None, 0, 0, None) == L.LI_ERR_INVALID_ARG
     # unsupported head dim / block size / dtype

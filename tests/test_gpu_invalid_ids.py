@@ -9,7 +9,8 @@ oracle run on the same lists with the invalid ids dropped.  Covered: the tiled
 bf16 kernel (whole tiles and the balanced order), the fused kernel (token
 order, with a text block), the tiled e4m3 kernel and the fused e4m3 kernel;
 invalid ids first, last, in the middle and filling a whole row (zeros, LSE
--inf).
+-inf).  Also the lists with nothing to read: index tensors with no columns,
+and split tiles whose second half is empty in a one-column index tensor.
 """
 import math
 
@@ -176,3 +177,75 @@ def test_e4m3_kernels_skip_invalid_ids(dev):
     torch.cuda.synchronize()
     _check(out_t, lse_t, o_ref, lse_ref, "tiled e4m3")
     _check(out_f, lse_f, _to_tokens(o_ref, c), lse_ref, "fused e4m3")
+
+
+def test_lists_without_columns_give_zeros(dev):
+    """Index tensors with no columns (every count clamps to 0): zeros and LSE -inf from the tiled kernel (with
+    and without the balanced order), the fused kernel and both e4m3 kernels.  An empty list runs as one block
+    with an out-of-range id, and its row has no entry to read."""
+    c = _grid_case(31, text=0)
+    H, D, nq = c["H"], c["D"], c["nq"]
+    print(f"[gpu] lists with no columns (nq={nq}, nkb={c['nkb']})", flush=True)
+    fq, fk, Hh, W, (tt, th, tw), nh, nw = c["geo"]
+    # zero-column view of a real allocation (a non-null pointer, n_cols = 0); counts above 0 clamp to 0
+    ii = torch.full((1, H, nq, 1), 3, dtype=torch.int32, device=dev)[..., :0]
+    cc = torch.full((1, H, nq), 2, dtype=torch.int32, device=dev)
+    scale = 1.0 / math.sqrt(D)
+    qf = torch.from_numpy(np.ascontiguousarray(c["qf"])).to(torch.bfloat16).to(dev)
+    kf = torch.from_numpy(np.ascontiguousarray(c["kf"])).to(torch.bfloat16).to(dev)
+    vf = torch.from_numpy(np.ascontiguousarray(c["vf"])).to(torch.bfloat16).to(dev)
+    outs = []
+    for balance in (False, True):
+        o, l = _core.bsa_forward(qf, kf, vf, ii, cc, scale, 128, return_lse=True, balance=balance)
+        outs.append((f"tiled balance={balance}", o, l))
+    qd, kd, vd = c["q"].to(dev), c["k"].to(dev), c["v"].to(dev)
+    o = torch.empty_like(qd)
+    _, l = _core.bsa_forward_gather(qd, kd, vd, None, None, 0, fq, fk, Hh, W, tt, th, tw, nh, nw, ii, cc, scale, o,
+                                    return_lse=True)
+    outs.append(("fused", o, l))
+    q8, qs, _ = _e4m3(c["qf"])
+    k8, ks, _ = _e4m3(c["kf"])
+    o, l = _core.bsa_forward_fp8(q8.to(dev), qs.to(dev), k8.to(dev), ks.to(dev), vf, ii, cc, scale, 128,
+                                 return_lse=True)
+    outs.append(("tiled e4m3", o, l))
+    o = torch.empty_like(qd)
+    _, l = _core.bsa_forward_fp8_gather(q8.to(dev), qs.to(dev), k8.to(dev), ks.to(dev), vd, None, 0, fq, fk, Hh, W,
+                                        tt, th, tw, nh, nw, ii, cc, scale, o, return_lse=True)
+    outs.append(("fused e4m3", o, l))
+    torch.cuda.synchronize()
+    for name, o, l in outs:
+        print(f"[gpu]   {name}: max |out| {o.float().abs().max().item():.3e}", flush=True)
+        assert o.float().abs().max().item() == 0.0
+        assert torch.isneginf(l).all()
+
+
+def test_split_tiles_with_an_empty_second_half(dev):
+    """Tail-split tiles whose lists hold 0 or 1 block in an index tensor of one column: the second half of a
+    one-block list is empty and its row has no entry left.  Split against whole tiles and the oracle."""
+    from li_sparse import _lib
+
+    bs, D, B, H, nq, nkb = 128, 128, 1, 8, 44, 6
+    Lq, Lk = nq * bs - 40, nkb * bs
+    with torch.cuda.device(dev):
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        ws = _lib.lib.li_bsa_fwd_workspace_size(B, H, Lq, D, bs)
+    print(f"[gpu] split tiles with one-column lists (B={B} H={H} Lq={Lq} Lk={Lk}, {cus} CUs)", flush=True)
+    rng = np.random.default_rng(17)
+    q, k, v = _bf16(41, (B, H, Lq, D), 0.2), _bf16(42, (B, H, Lk, D)), _bf16(43, (B, H, Lk, D))
+    ind = rng.integers(0, nkb, size=(B, H, nq, 1)).astype(np.int32)
+    cnt = rng.integers(0, 2, size=(B, H, nq)).astype(np.int32)
+    cnt[0, H - 1, nq - 1] = 1          # the tensor's last row: its second half would start past the end
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    ii, cc = torch.from_numpy(ind).to(dev), torch.from_numpy(cnt).to(dev)
+    scale = 1.0 / math.sqrt(D)
+    out_s, lse_s = _core.bsa_forward(qd, kd, vd, ii, cc, scale, bs, return_lse=True, split=True)
+    out_w, lse_w = _core.bsa_forward(qd, kd, vd, ii, cc, scale, bs, return_lse=True, split=False)
+    torch.cuda.synchronize()
+    assert ws > 0
+    f64 = lambda t: bf16_to_f32(bits(t)).astype(np.float64)  # noqa: E731
+    o_ref, lse_ref = oatt.bsa_forward(f64(q), f64(k), f64(v), ind, cnt, scale, bs)
+    d_out = (out_s.float() - out_w.float()).abs().max().item()
+    print(f"[gpu]   split vs whole {d_out:.3e}", flush=True)
+    assert d_out <= 1e-2
+    assert torch.equal(torch.isneginf(lse_s), torch.isneginf(lse_w))
+    _check(out_s, lse_s, o_ref, lse_ref, "split")
