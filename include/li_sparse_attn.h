@@ -105,6 +105,12 @@ int li_pool(int dtype, int32_t B, int32_t NH, int32_t D,
  * HYAR:330-361), for the fused path.  When one job has no blocks or their
  * sources differ in vector access (16-byte aligned unit-stride rows), the
  * jobs are launched one after the other.
+ *   mean1_normalized: optional (NULL), same shape and strides as mean1: each
+ *     pooled row of job 1 divided by its L2 norm as the cosine metric of
+ *     li_block_mask normalises a key pool row (HYAR:250-252), same bits; the
+ *     block mask takes it with li_mask_params.k_normalized set, so the
+ *     normalisation runs once per key block rather than once per workgroup
+ *     of query rows.
  */
 int li_pool_pair(int dtype, int32_t B, int32_t NH, int32_t D,
                  const void* src0, const int64_t src0_strides[4],
@@ -112,7 +118,7 @@ int li_pool_pair(int dtype, int32_t B, int32_t NH, int32_t D,
                  const li_tile_geom* geom0,
                  const void* src1, const int64_t src1_strides[4],
                  void* mean1, const int64_t mean1_strides[4], int64_t pool_off1,
-                 const li_tile_geom* geom1, void* stream);
+                 const li_tile_geom* geom1, void* mean1_normalized, void* stream);
 
 /*
  * Untile scatter.  Replaces launch_untile(src, dst, T, H, W, tt, th, tw, nh, nw)
@@ -146,6 +152,8 @@ typedef struct li_mask_params {
   int32_t kmax;             /* row length of `indices` (>= num_txt_blk + largest budget) */
   const int32_t* row_budget;/* optional device (nq,) per-row visual totals (ragged rows); NULL = rule */
   float scale;              /* 1/sqrt(D) for LI_METRIC_SCALED_DOT, as fp32 */
+  int32_t k_normalized;     /* LI_METRIC_COSINE: k_pool rows are already normalised
+                               (li_pool_pair's mean1_normalized); 0 = raw pooled means */
 } li_mask_params;
 
 /*

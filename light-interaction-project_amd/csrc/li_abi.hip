@@ -13,7 +13,7 @@ void li::record_launch_error(hipError_t e) {
 
 extern "C" const char* li_last_error(void) { return g_last_error; }
 
-extern "C" int li_abi_version(void) { return 10; }
+extern "C" int li_abi_version(void) { return 11; }
 
 extern "C" const char* li_status_string(int status) {
   switch (status) {

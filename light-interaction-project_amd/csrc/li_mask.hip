@@ -251,7 +251,7 @@ __global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a, int waves) 
       float x[D];
       load_row<E, D>(kbase + (int64_t)j * a.ks[2], a.ks[3], vec, x);
       float dot = 0.0f;
-      if (cosine) {
+      if (cosine && !p.k_normalized) {
         const float den = norm_den<E, D>(x);
 #pragma unroll
         for (int d = 0; d < D; ++d) dot = dot + qv[d] * E::to_f32(E::from_f32(x[d] / den));
@@ -342,7 +342,7 @@ __global__ __launch_bounds__(512) void block_mask_tiled_kernel(MaskArgs a) {
     }
     __syncthreads();
     if (j0 + NT < nk) fetch(j0 + NT);
-    if (cosine) {
+    if (cosine && !p.k_normalized) {
       if (tid < nt) {
         uint8_t* krow = ktile + tid * RS;
         float ss = 0.0f;

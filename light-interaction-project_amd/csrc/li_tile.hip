@@ -29,6 +29,9 @@ struct GatherArgs {
   int64_t ds[2][5];
   uint16_t* mean;
   int64_t ms[4];
+  // Optional second pool output (strides ms): each pooled row divided by its
+  // L2 norm as the cosine block-mask metric normalises it.
+  uint16_t* mean_n;
   int64_t dst_off, pool_off;
   int32_t NH, bs;
   li_tile_geom g;
@@ -142,6 +145,7 @@ __device__ __forceinline__ void gather_pool_block(const GatherArgs& a, int blk, 
 #pragma unroll
   for (int i = 0; i < 8; ++i) red[g0][8 * c + i] = acc[i];
   __syncthreads();
+  float mrow = 0.0f;
   if (tid < D) {
     float s[NG];
 #pragma unroll
@@ -153,6 +157,28 @@ __device__ __forceinline__ void gather_pool_block(const GatherArgs& a, int blk, 
     }
     const float mean = s[0] / (float)a.bs;
     a.mean[b * a.ms[0] + h * a.ms[1] + (blk + a.pool_off) * a.ms[2] + (int64_t)tid * a.ms[3]] = E::from_f32(mean);
+    mrow = E::to_f32(E::from_f32(mean));
+  }
+  if (a.mean_n) {
+    // The cosine metric's normalisation of the rounded row: sequential fp32
+    // sum of squares over d from +0.0, x / max(E(sqrt(.)), E(1e-12)), the
+    // arithmetic the block mask applies to a raw key pool row.
+    __syncthreads();  // the partial sums are read
+    if (tid < D) red[0][tid] = mrow;
+    __syncthreads();
+    // Wave 0 alone finishes the row (every lane runs the same chain over
+    // broadcast reads); the other waves end here and free their slots.
+    if (tid >= 64) return;
+    float ss = 0.0f;
+#pragma unroll
+    for (int d = 0; d < D; ++d) ss = ss + red[0][d] * red[0][d];
+    const float nrm = E::to_f32(E::from_f32(__builtin_sqrtf(ss)));
+    const float eps = E::to_f32(E::from_f32(1e-12f));
+    const float den = nrm > eps ? nrm : eps;
+#pragma unroll
+    for (int d = tid; d < D; d += 64)
+      a.mean_n[b * a.ms[0] + h * a.ms[1] + (blk + a.pool_off) * a.ms[2] + (int64_t)d * a.ms[3]] =
+          E::from_f32(red[0][d] / den);
   }
 }
 
@@ -668,10 +694,12 @@ extern "C" int li_pool_pair(int dtype, int32_t B, int32_t NH, int32_t D, const v
                             const int64_t src0_strides[4], void* mean0, const int64_t mean0_strides[4],
                             int64_t pool_off0, const li_tile_geom* geom0, const void* src1,
                             const int64_t src1_strides[4], void* mean1, const int64_t mean1_strides[4],
-                            int64_t pool_off1, const li_tile_geom* geom1, void* stream) {
+                            int64_t pool_off1, const li_tile_geom* geom1, void* mean1_normalized,
+                            void* stream) {
   GatherArgs a0, a1;
   if (!pool_job(a0, src0, src0_strides, mean0, mean0_strides, pool_off0) ||
       !pool_job(a1, src1, src1_strides, mean1, mean1_strides, pool_off1))
     return LI_ERR_INVALID_ARG;
+  a1.mean_n = static_cast<uint16_t*>(mean1_normalized);
   return launch_pool_pair(dtype, B, NH, D, a0, geom0, a1, geom1, static_cast<hipStream_t>(stream));
 }

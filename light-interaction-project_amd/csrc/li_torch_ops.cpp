@@ -98,12 +98,21 @@ void pool(const at::Tensor& src, at::Tensor& mean, int64_t pool_off, c10::IntArr
 }
 
 void pool_pair(const at::Tensor& src0, at::Tensor& mean0, int64_t off0, c10::IntArrayRef geom0,
-               const at::Tensor& src1, at::Tensor& mean1, int64_t off1, c10::IntArrayRef geom1) {
+               const at::Tensor& src1, at::Tensor& mean1, int64_t off1, c10::IntArrayRef geom1,
+               const c10::optional<at::Tensor>& mean1_normalized) {
   gpu(src0, "src0");
   rank(src0, 4, "src0");
   rank(src1, 4, "src1");
   rank(mean0, 4, "mean0");
   rank(mean1, 4, "mean1");
+  void* mean1_n = nullptr;
+  if (mean1_normalized.has_value() && mean1_normalized->defined()) {
+    const at::Tensor& t = *mean1_normalized;
+    TORCH_CHECK(t.sizes() == mean1.sizes() && t.strides() == mean1.strides() && t.scalar_type() == mean1.scalar_type() &&
+                    t.device() == mean1.device(),
+                "mean1_normalized must match mean1 in shape, strides, dtype and device");
+    mean1_n = t.data_ptr();
+  }
   c10::DeviceGuard guard(src0.device());
   const li_tile_geom g0 = geom_of(geom0), g1 = geom_of(geom1);
   const auto s0 = strides<4>(src0);
@@ -113,7 +122,7 @@ void pool_pair(const at::Tensor& src0, at::Tensor& mean0, int64_t off0, c10::Int
   check("li_pool_pair",
         li_pool_pair(dtype_code(src0), (int32_t)src0.size(0), (int32_t)src0.size(1), (int32_t)src0.size(3),
                      src0.data_ptr(), s0.data(), mean0.data_ptr(), m0.data(), off0, &g0, src1.data_ptr(), s1.data(),
-                     mean1.data_ptr(), m1.data(), off1, &g1, stream_of(src0)));
+                     mean1.data_ptr(), m1.data(), off1, &g1, mean1_n, stream_of(src0)));
 }
 
 void q_prep(const at::Tensor& src, at::Tensor& dst, at::Tensor& mean, c10::IntArrayRef geom) {
@@ -170,7 +179,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> block_mask(const at::Tensor& q_po
                                                           bool force_sink, bool force_neighbors, int64_t nh,
                                                           int64_t nw, int64_t num_txt_blk, int64_t kmax,
                                                           const c10::optional<at::Tensor>& row_budget,
-                                                          bool return_scores) {
+                                                          bool return_scores, bool k_normalized) {
   gpu(q_pool, "q_pool");
   rank(q_pool, 4, "q_pool");
   rank(k_pool, 4, "k_pool");
@@ -203,6 +212,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> block_mask(const at::Tensor& q_po
     p.row_budget = row_budget->data_ptr<int32_t>();
   }
   p.scale = (float)(1.0 / std::sqrt((double)D));
+  p.k_normalized = k_normalized;
   const auto qs = strides<4>(q_pool);
   const auto ks = strides<4>(k_pool);
   check("li_block_mask", li_block_mask(dtype_code(q_pool), (int32_t)B, (int32_t)NH, (int32_t)D, q_pool.data_ptr(),
@@ -417,14 +427,14 @@ at::Tensor bsa_fwd_fp8_gather(const at::Tensor& q8, const at::Tensor& q_scale, c
 TORCH_LIBRARY(li, m) {
   m.def("pool(Tensor src, Tensor(a!) mean, int pool_off, int[] geom) -> ()");
   m.def("pool_pair(Tensor src0, Tensor(a!) mean0, int pool_off0, int[] geom0, Tensor src1, Tensor(b!) mean1, "
-        "int pool_off1, int[] geom1) -> ()");
+        "int pool_off1, int[] geom1, Tensor(c!)? mean1_normalized=None) -> ()");
   m.def("q_prep(Tensor src, Tensor(a!) dst, Tensor(b!) mean, int[] geom) -> ()");
   m.def("kv_prep(Tensor k_src, Tensor v_src, Tensor(a!) k_dst, Tensor(b!) v_dst, Tensor(c!) k_mean, int dst_off, "
         "int pool_off, int[] geom) -> ()");
   m.def("untile(Tensor src, Tensor(a!) dst, int[] geom) -> ()");
   m.def("block_mask(Tensor q_pool, Tensor k_pool, int metric, int budget_mode, float ratio, int min_budget, "
         "int n_recent, bool force_diag, bool force_sink, bool force_neighbors, int nh, int nw, int num_txt_blk, "
-        "int kmax, Tensor? row_budget, bool return_scores) -> (Tensor, Tensor, Tensor)");
+        "int kmax, Tensor? row_budget, bool return_scores, bool k_normalized=False) -> (Tensor, Tensor, Tensor)");
   m.def("bsa_fwd(Tensor q, Tensor k, Tensor v, Tensor indices, Tensor counts, float sm_scale, int block_size, "
         "Tensor(a!) out, bool return_lse, bool split, bool balance) -> Tensor");
   m.def("bsa_fwd_gather(Tensor q, Tensor k, Tensor v, Tensor? k_txt, Tensor? v_txt, int num_txt_blk, int[] q_geom, "

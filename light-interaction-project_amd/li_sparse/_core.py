@@ -169,13 +169,20 @@ def pool(src, mean, pool_off, T, H, W, tt, th, tw, nh, nw):
     _run(ops.pool, src, mean, int(pool_off), [T, H, W, tt, th, tw, nh, nw])
 
 
-def pool_pair(src0, mean0, pool_off0, geom0, src1, mean1, pool_off1, geom1):
+def pool_pair(src0, mean0, pool_off0, geom0, src1, mean1, pool_off1, geom1, mean1_normalized=None):
     """Two pools (see li_pool_pair) in one launch; geom = (T, H, W, tt, th, tw, nh, nw) of each job.
 
-    Same values, bit for bit, as ``pool`` on each job.
+    Same values, bit for bit, as ``pool`` on each job.  ``mean1_normalized`` (optional, the shape and
+    strides of ``mean1``) also receives job 1's rows normalised as the cosine block mask normalises a
+    key pool row.
     """
     _device_check(src0, mean0, src1, mean1)
     _same_dtype(src0, mean0, src1, mean1)
+    if mean1_normalized is not None:
+        _device_check(mean1, mean1_normalized)
+        _same_dtype(mean1, mean1_normalized)
+        if mean1_normalized.shape != mean1.shape or mean1_normalized.stride() != mean1.stride():
+            raise ValueError("mean1_normalized must have the shape and strides of mean1")
     B, NH, _, D = src0.shape
     if tuple(src1.shape[:2]) != (B, NH) or src1.shape[3] != D:
         raise ValueError(f"pool pair sources {tuple(src0.shape)} and {tuple(src1.shape)} differ in B, NH or D")
@@ -189,7 +196,15 @@ def pool_pair(src0, mean0, pool_off0, geom0, src1, mean1, pool_off1, geom1):
             raise ValueError(f"pool buffer shape {tuple(mean.shape)} does not hold {nblk}+{off} rows of {D}")
         gs.append([int(x) for x in geo])
     dtype_code(src0)
-    _run(ops.pool_pair, src0, mean0, int(pool_off0), gs[0], src1, mean1, int(pool_off1), gs[1])
+    _run(ops.pool_pair, src0, mean0, int(pool_off0), gs[0], src1, mean1, int(pool_off1), gs[1], mean1_normalized)
+
+
+def attach_normalized(k_pool, k_pool_normalized):
+    """Mark ``k_pool_normalized`` as ``k_pool`` with every row normalised for the cosine metric (as
+    ``pool_pair``'s ``mean1_normalized`` writes it); ``block_mask`` with ``metric="cosine"`` then scores
+    against it instead of normalising every key row once per workgroup of query rows (same bits).  The
+    writer of ``k_pool`` keeps the two in step."""
+    k_pool.li_normalized = k_pool_normalized
 
 
 def fused_supported(D, tile, latent_hw):
@@ -364,7 +379,8 @@ def block_mask(q_pool, k_pool, *, metric, budget_mode, ratio, nh, nw, num_txt_bl
     """Block selection on the device (see li_block_mask).
 
     Returns ``(indices (B,H,nq,kmax) int32, counts (B,H,nq) int32)`` (+ scores if asked), where
-    ``kmax = num_txt_blk + max row budget``.
+    ``kmax = num_txt_blk + max row budget``.  With ``metric="cosine"``, a ``k_pool`` that carries its
+    normalised copy (``attach_normalized``) is scored through that copy.
     """
     dev = _device_check(q_pool, k_pool)
     _same_dtype(q_pool, k_pool)
@@ -376,10 +392,15 @@ def block_mask(q_pool, k_pool, *, metric, budget_mode, ratio, nh, nw, num_txt_bl
     kmax, rb_dev = _mask_plan(dev, nq, nk, nh, nw, num_txt_blk, n_recent, bool(force_diag), bool(force_sink),
                               bool(force_neighbors), budget_mode, float(ratio), int(min_budget), row_budget)
     dtype_code(q_pool)
+    k_norm = getattr(k_pool, "li_normalized", None) if metric_code == _lib.LI_METRIC_COSINE else None
+    if k_norm is not None:
+        if k_norm.shape != k_pool.shape or k_norm.dtype != k_pool.dtype or k_norm.device != k_pool.device:
+            raise ValueError("the normalised key pool does not match the key pool")
+        k_pool = k_norm
     indices, counts, scores = _run(ops.block_mask, q_pool, k_pool, metric_code, int(budget_mode), float(ratio),
                                              int(min_budget), int(n_recent), bool(force_diag), bool(force_sink),
                                              bool(force_neighbors), int(nh), int(nw), int(num_txt_blk), int(kmax),
-                                             rb_dev, bool(return_scores))
+                                             rb_dev, bool(return_scores), k_norm is not None)
     if return_scores:
         return indices, counts, scores
     return indices, counts

@@ -16,7 +16,7 @@ import os
 import torch  # noqa: F401  (must precede the CDLL below)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libli_sparse_attn.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 LI_OK = 0
 LI_ERR_INVALID_ARG = -1
@@ -56,7 +56,8 @@ class MaskParams(ctypes.Structure):
     _fields_ = [("metric", _i32), ("budget_mode", _i32), ("topk_ratio", ctypes.c_double),
                 ("min_budget", _i32), ("n_recent", _i32), ("force_diag", _i32), ("force_sink", _i32),
                 ("force_neighbors", _i32), ("nq", _i32), ("nk", _i32), ("nh", _i32), ("nw", _i32),
-                ("num_txt_blk", _i32), ("kmax", _i32), ("row_budget", _vp), ("scale", ctypes.c_float)]
+                ("num_txt_blk", _i32), ("kmax", _i32), ("row_budget", _vp), ("scale", ctypes.c_float),
+                ("k_normalized", _i32)]
 
 
 # name -> (restype, argtypes); mirrors include/li_sparse_attn.h
@@ -98,7 +99,7 @@ SIGNATURES = {
                                ctypes.POINTER(TileGeom), _vp]),
     "li_pool_pair": (ctypes.c_int, [ctypes.c_int, _i32, _i32, _i32, _vp, _i64p, _vp, _i64p, _i64,
                                     ctypes.POINTER(TileGeom), _vp, _i64p, _vp, _i64p, _i64,
-                                    ctypes.POINTER(TileGeom), _vp]),
+                                    ctypes.POINTER(TileGeom), _vp, _vp]),
 }
 
 

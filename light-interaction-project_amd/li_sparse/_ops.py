@@ -56,7 +56,7 @@ def _pool_fake(src, mean, pool_off, geom):
 
 
 @torch.library.register_fake("li::pool_pair")
-def _pool_pair_fake(src0, mean0, pool_off0, geom0, src1, mean1, pool_off1, geom1):
+def _pool_pair_fake(src0, mean0, pool_off0, geom0, src1, mean1, pool_off1, geom1, mean1_normalized=None):
     return None
 
 
@@ -77,7 +77,7 @@ def _untile_fake(src, dst, geom):
 
 @torch.library.register_fake("li::block_mask")
 def _block_mask_fake(q_pool, k_pool, metric, budget_mode, ratio, min_budget, n_recent, force_diag, force_sink,
-                     force_neighbors, nh, nw, num_txt_blk, kmax, row_budget, return_scores):
+                     force_neighbors, nh, nw, num_txt_blk, kmax, row_budget, return_scores, k_normalized=False):
     B, NH, nq, _ = q_pool.shape
     nk = k_pool.shape[2]
     indices = q_pool.new_empty((B, NH, nq, kmax), dtype=torch.int32)

@@ -83,6 +83,11 @@ def qk_fp8(sparse_params):
     return bool(sparse_params.get("qk_fp8", False))
 
 
+def cosine(sparse_params):
+    """Whether the selection scores blocks by cosine similarity (the reference's default ``sim_metric``)."""
+    return sparse_params.get("sim_metric", "cosine") == "cosine"
+
+
 class ContextCache:
     """Prepared key-side blocks of the fixed context of K/V, kept across calls.
 
@@ -126,22 +131,28 @@ def _pad_text(x, g, text_len):
     return (F.pad(x, (0, 0, 0, pad)) if pad > 0 else x).contiguous()
 
 
-def _k_side(path, k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, dt, q_pool_job=None):
+def _k_side(path, k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, dt, q_pool_job=None, k_norm=False):
     """Key-side buffers of one call: text blocks, then the visual blocks from the first uncached frame.
 
     path: "fused" (K pool; padded text K/V), "fused_fp8" (e4m3 K tiles + scales, K pool; padded text V),
     "tiled" (K/V tiles, K pool), "tiled_fp8" (e4m3 K tiles + scales, V tiles, K pool).
     q_pool_job: (q, q_pool, pool_off, geometry) of the query pool, taken in the same launch as the K pool on
     the fused path (li_pool_pair), or on its own when there is no K pool to take (every frame cached).
+    k_norm: on the fused path, also keep the K pool's rows normalised for the cosine selection (written by
+    the same launch and attached to the K pool, see _core.attach_normalized).
     """
     cache, layer, cframes = ctx if ctx is not None else (None, None, 0)
     cf = min((max(cframes, 0) // g.tt) * g.tt, g.T_k) if cache is not None else 0
-    key = (path, layer, B, NH, D, dt, str(dev), g, text_len, cf)
+    k_norm = bool(k_norm) and path == "fused"
+    key = (path, layer, B, NH, D, dt, str(dev), g, text_len, cf, k_norm)
     bufs = cache._entries.get(key) if cache is not None else None
     first = cf if bufs is not None else 0
     nkb = g.num_txt_blk + g.nk_blk
     if bufs is None:
-        bufs = {"k_pool": torch.empty((B, NH, g.nk_blk, D), device=dev, dtype=dt)}
+        bufs = {"k_pool": torch.empty((B, NH, g.nk_blk, D), device=dev, dtype=dt), "k_pool_n": None}
+        if k_norm:
+            bufs["k_pool_n"] = torch.empty_like(bufs["k_pool"])
+            _core.attach_normalized(bufs["k_pool"], bufs["k_pool_n"])
         if path in ("fused_fp8", "tiled_fp8"):
             bufs["k8"] = torch.empty((B, NH, nkb, g.bs, D), device=dev, dtype=_core.FP8)
             bufs["k_scale"] = torch.empty((B, NH, nkb), device=dev, dtype=torch.float32)
@@ -173,9 +184,11 @@ def _k_side(path, k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, d
         kv, vv = k_vis[:, :, tok:], v_vis[:, :, tok:]
         geo = (T, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw)
         if path == "fused" and q_pool_job is not None:
-            _core.pool_pair(*q_pool_job, kv, bufs["k_pool"], fb, geo)
+            _core.pool_pair(*q_pool_job, kv, bufs["k_pool"], fb, geo, mean1_normalized=bufs["k_pool_n"])
             q_pool_job = None
         elif path == "fused":
+            if k_norm:
+                raise ValueError("the normalised key pool is written with the query pool (li_pool_pair)")
             _core.pool(kv, bufs["k_pool"], fb, *geo)
         elif path == "fused_fp8":
             _core.tile_prep_fp8(kv, bufs["k8"], bufs["k_scale"], bufs["k_pool"], g.num_txt_blk + fb, fb, *geo)
@@ -190,7 +203,7 @@ def _k_side(path, k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, d
     return bufs
 
 
-def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance, ctx):
+def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance, ctx, k_norm=False):
     """Pools, block selection, then one kernel that gathers, attends and untiles."""
     B, NH, _, D = q.shape
     dev, dt = q.device, q.dtype
@@ -200,7 +213,8 @@ def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events
     _stage(events, "alloc_end")
     _stage(events, "prep_start")
     q_job = (q, q_pool, 0, (g.T_q, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw))
-    kb = _k_side("fused", k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, dt, q_pool_job=q_job)
+    kb = _k_side("fused", k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, dt, q_pool_job=q_job,
+                 k_norm=k_norm)
     _stage(events, "prep_end")
     _stage(events, "index_start")
     indices, counts = select(q_pool, kb["k_pool"], text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
@@ -281,7 +295,7 @@ def _fused_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, ev
 
 
 def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, events=None, fused=True,
-                     balance=False, qk_fp8=False, context=None):
+                     balance=False, qk_fp8=False, context=None, normalize_k_pool=False):
     """One sparse-attention forward.
 
     q (B,H,Lq,D); k_txt/v_txt (B,H,N_txt,D) or None; k_vis/v_vis (B,H,Lk,D), any strides.
@@ -297,7 +311,10 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
     the longest query tiles first.  ``qk_fp8`` takes Q K^T on e4m3 codes with one scale per tile
     block (bf16 only; D = 128 and 128-token tiles, ValueError otherwise); the selection is unchanged.
     ``context`` = (ContextCache, layer key, context frames) keeps the key-side preparation of the
-    fixed leading frames and the text across calls (see ContextCache).
+    fixed leading frames and the text across calls (see ContextCache).  ``normalize_k_pool`` (``select``
+    scores by cosine similarity): the fused bf16/f16 path's pool launch also writes the key pool's rows
+    normalised, once per key block, and the block mask takes them instead of normalising every key row in
+    every workgroup of query rows (same selection, bit for bit).
     """
     out_dtype = q.dtype
     if q.dtype not in (torch.bfloat16, torch.float16):
@@ -317,7 +334,7 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
             return _fused_fp8(*args)
         return _tiled_fp8(*args)
     if fused and uses_fused(q, k_vis, v_vis, tile, (g.H, g.W)):
-        return _fused(*args)
+        return _fused(*args, k_norm=normalize_k_pool)
     _stage(events, "alloc_start")
     q_tiled = torch.empty((B, NH, g.nq_blk, g.bs, D), device=dev, dtype=dt)
     q_pool = torch.empty((B, NH, g.nq_blk, D), device=dev, dtype=dt)

@@ -69,4 +69,5 @@ def run_sparse_attention(q, k_txt, v_txt, k_vis, v_vis, block_idx, latent_hw, sp
     return _pipeline.sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select,
                                       balance=_pipeline.ragged(sparse_params),
                                       qk_fp8=_pipeline.qk_fp8(sparse_params),
-                                      context=_pipeline.context_of(sparse_params, block_idx))
+                                      context=_pipeline.context_of(sparse_params, block_idx),
+                                      normalize_k_pool=_pipeline.cosine(sparse_params))

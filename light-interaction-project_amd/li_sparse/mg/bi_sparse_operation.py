@@ -44,7 +44,8 @@ def run_sparse_attention(q, k, v, text_len, block_idx, latent_hw, sparse_params)
     o = _pipeline.sparse_attention(q, k_txt, v_txt, k[:, :, text_len:], v[:, :, text_len:], latent_hw, tile,
                                    select, events, balance=_pipeline.ragged(sparse_params),
                                    qk_fp8=_pipeline.qk_fp8(sparse_params),
-                                   context=_pipeline.context_of(sparse_params, block_idx))
+                                   context=_pipeline.context_of(sparse_params, block_idx),
+                                   normalize_k_pool=_pipeline.cosine(sparse_params))
     if events is not None:
         torch.cuda.synchronize()
         t = lambda a, b: events[a].elapsed_time(events[b])  # noqa: E731

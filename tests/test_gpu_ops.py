@@ -54,6 +54,7 @@ def test_opcheck_prep_and_mask_ops(dev):
     qp = torch.empty((1, 2, 4, 128), dtype=torch.bfloat16, device=dev)
     kp = torch.empty((1, 2, 8, 128), dtype=torch.bfloat16, device=dev)
     torch.library.opcheck(ops.pool_pair.default, (q, qp, 0, gq, k, kp, 0, gk))
+    torch.library.opcheck(ops.pool_pair.default, (q, qp, 0, gq, k, kp, 0, gk, torch.empty_like(kp)))
     qt = torch.empty((1, 2, 4, 128, 128), dtype=torch.bfloat16, device=dev)
     torch.library.opcheck(ops.q_prep.default, (q, qt, qp, gq))
     kt, vt = (torch.empty((1, 2, 8, 128, 128), dtype=torch.bfloat16, device=dev) for _ in range(2))
@@ -65,6 +66,8 @@ def test_opcheck_prep_and_mask_ops(dev):
     kp.copy_(torch.randn(kp.shape, generator=g).to(kp.dtype))
     torch.library.opcheck(ops.block_mask.default,
                           (qp, kp, 1, 0, 0.5, 7, 0, True, True, False, 2, 2, 0, 8, None, True))
+    torch.library.opcheck(ops.block_mask.default,
+                          (qp, kp, 0, 0, 0.5, 7, 0, True, True, False, 2, 2, 0, 8, None, True, True))
 
 
 def test_compiled_graph_calls_the_ops(dev):

@@ -24,7 +24,7 @@ def test_mutation_annotations():
                 if a.alias_info is not None and a.alias_info.is_write]
     assert written("q_prep") == ["dst", "mean"]
     assert written("kv_prep") == ["k_dst", "v_dst", "k_mean"]
-    assert written("pool_pair") == ["mean0", "mean1"]
+    assert written("pool_pair") == ["mean0", "mean1", "mean1_normalized"]
     assert written("untile") == ["dst"]
     assert written("bsa_fwd") == written("bsa_fwd_gather") == written("attn_dense") == ["out"]
     assert written("block_mask") == []
