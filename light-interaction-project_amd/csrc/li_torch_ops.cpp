@@ -1,12 +1,15 @@
 // PyTorch custom operators torch.ops.li.* over the C ABI of libli_sparse_attn.so.
 //
-// Each operator checks dtypes and ranks, allocates what it returns (and the
-// attention workspace) through the caching allocator, writes the tensors its
-// schema marks as mutated (Tensor(a!): tiles, pools, attention outputs), and
-// enqueues the C-ABI call on torch's current HIP stream of the tensors' device.  Shape rules and
-// the reference's error messages stay in the Python wrappers that call these
-// operators (li_sparse/_core.py); the fake (meta) implementations, which give
-// output shapes for tracing, are registered in li_sparse/_ops.py.
+// Each operator checks dtypes, ranks, devices and every tensor's extent
+// against the geometry and lists it is indexed by (so that a direct call
+// cannot make a kernel read or write past a tensor), allocates what it
+// returns (and the attention workspace) through the caching allocator, writes
+// the tensors its schema marks as mutated (Tensor(a!): tiles, pools, attention
+// outputs), and enqueues the C-ABI call on torch's current HIP stream of the
+// tensors' device.  The reference's error messages stay in the Python
+// wrappers that call these operators (li_sparse/_core.py); the fake (meta)
+// implementations, which give output shapes for tracing, are registered in
+// li_sparse/_ops.py.
 //
 // Reference interfaces replaced (paths relative to the reference repository):
 //   hy-worldplay/files/hyvideo/models/transformers/modules/ar_sparse_operation.py:166-218 (launch_q_prep,
@@ -49,6 +52,8 @@ void rank(const at::Tensor& t, int64_t r, const char* name) {
 
 li_tile_geom geom_of(c10::IntArrayRef g) {
   TORCH_CHECK(g.size() == 8, "geometry must be (T, H, W, tt, th, tw, nh, nw)");
+  TORCH_CHECK(g[0] >= 0 && g[1] > 0 && g[2] > 0 && g[3] > 0 && g[4] > 0 && g[5] > 0 && g[6] > 0 && g[7] > 0,
+              "geometry (T, H, W, tt, th, tw, nh, nw) must have T >= 0 and the other fields positive, got ", g);
   li_tile_geom r;
   r.T = (int32_t)g[0];
   r.H = (int32_t)g[1];
@@ -83,6 +88,72 @@ at::Tensor lse_or_empty(const at::Tensor& like, bool want, int64_t B, int64_t NH
   return at::empty(want ? c10::IntArrayRef({B, NH, rows}) : c10::IntArrayRef({0}), like.options().dtype(at::kFloat));
 }
 
+// Extent checks.  The C ABI takes pointers and strides only, so these are
+// what keeps a direct call of an operator (outside the Python wrappers) from
+// reading or writing past a tensor: every tensor must reach at least as far
+// as the kernels index it, on the device of the first one.
+
+int64_t blocks_of(const li_tile_geom& g) { return (int64_t)((g.T + g.tt - 1) / g.tt) * g.nh * g.nw; }
+int64_t tokens_of(const li_tile_geom& g) { return (int64_t)g.T * g.H * g.W; }
+int64_t block_size_of(const li_tile_geom& g) { return (int64_t)g.tt * g.th * g.tw; }
+
+void on_device(const at::Tensor& ref, const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.device() == ref.device(), name, " must be on ", ref.device(), ", got ", t.device());
+}
+
+// (B, NH, >= rows, D), with the element type of `like` when given.
+void rows4(const at::Tensor& t, int64_t B, int64_t NH, int64_t rows, int64_t D, const char* name,
+           const at::Tensor* like = nullptr) {
+  TORCH_CHECK(t.dim() == 4 && t.size(0) == B && t.size(1) == NH && t.size(2) >= rows && t.size(3) == D, name,
+              " must be (", B, ", ", NH, ", >= ", rows, ", ", D, "), got ", t.sizes());
+  if (like) {
+    on_device(*like, t, name);
+    TORCH_CHECK(t.scalar_type() == like->scalar_type(), name, " must be ", like->scalar_type(), ", got ",
+                t.scalar_type());
+  }
+}
+
+// (B, NH, >= blocks, BS, D) tiles.
+void tiles5(const at::Tensor& t, int64_t B, int64_t NH, int64_t blocks, int64_t BS, int64_t D, const char* name,
+            const at::Tensor& ref) {
+  TORCH_CHECK(t.dim() == 5 && t.size(0) == B && t.size(1) == NH && t.size(2) >= blocks && t.size(3) == BS &&
+                  t.size(4) == D,
+              name, " must be (", B, ", ", NH, ", >= ", blocks, ", ", BS, ", ", D, "), got ", t.sizes());
+  on_device(ref, t, name);
+}
+
+// (B, NH, >= blocks) fp32 scales.
+void scales3(const at::Tensor& t, int64_t B, int64_t NH, int64_t blocks, const char* name, const at::Tensor& ref) {
+  TORCH_CHECK(t.dim() == 3 && t.size(0) == B && t.size(1) == NH && t.size(2) >= blocks &&
+                  t.scalar_type() == at::kFloat,
+              name, " must be float32 (", B, ", ", NH, ", >= ", blocks, "), got ", t.scalar_type(), " ", t.sizes());
+  on_device(ref, t, name);
+}
+
+void codes(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.element_size() == 1, name, " must hold 1-byte e4m3 codes, got ", t.scalar_type());
+}
+
+// Lists over nq query tiles: indices (B, NH, nq, n_cols), counts (B, NH, nq), int32.
+void lists(const at::Tensor& indices, const at::Tensor& counts, int64_t B, int64_t NH, int64_t nq,
+           const at::Tensor& ref) {
+  TORCH_CHECK(indices.size(0) == B && indices.size(1) == NH && indices.size(2) >= nq, "block_indices must be (",
+              B, ", ", NH, ", >= ", nq, ", n), got ", indices.sizes());
+  TORCH_CHECK(counts.size(0) == B && counts.size(1) == NH && counts.size(2) >= nq, "block_counts must be (", B,
+              ", ", NH, ", >= ", nq, "), got ", counts.sizes());
+  on_device(ref, indices, "block_indices");
+  on_device(ref, counts, "block_counts");
+}
+
+// Contiguous text rows (B, NH, >= rows, D) when there are any.
+void text(const c10::optional<at::Tensor>& t, int64_t rows, int64_t B, int64_t NH, int64_t D, const char* name,
+          const at::Tensor& like) {
+  if (rows <= 0) return;
+  TORCH_CHECK(t.has_value() && t->defined(), name, " is required with text blocks");
+  TORCH_CHECK(t->is_contiguous(), name, " must be contiguous");
+  rows4(*t, B, NH, rows, D, name, &like);
+}
+
 // ---------------------------------------------------------------------------
 
 void pool(const at::Tensor& src, at::Tensor& mean, int64_t pool_off, c10::IntArrayRef geom) {
@@ -91,6 +162,9 @@ void pool(const at::Tensor& src, at::Tensor& mean, int64_t pool_off, c10::IntArr
   rank(mean, 4, "mean");
   c10::DeviceGuard guard(src.device());
   const li_tile_geom g = geom_of(geom);
+  const int64_t B = src.size(0), NH = src.size(1), D = src.size(3);
+  rows4(src, B, NH, tokens_of(g), D, "src");
+  rows4(mean, B, NH, blocks_of(g) + pool_off, D, "mean", &src);
   const auto ss = strides<4>(src);
   const auto ms = strides<4>(mean);
   check("li_pool", li_pool(dtype_code(src), (int32_t)src.size(0), (int32_t)src.size(1), (int32_t)src.size(3),
@@ -115,6 +189,13 @@ void pool_pair(const at::Tensor& src0, at::Tensor& mean0, int64_t off0, c10::Int
   }
   c10::DeviceGuard guard(src0.device());
   const li_tile_geom g0 = geom_of(geom0), g1 = geom_of(geom1);
+  {
+    const int64_t B = src0.size(0), NH = src0.size(1), D = src0.size(3);
+    rows4(src0, B, NH, tokens_of(g0), D, "src0");
+    rows4(mean0, B, NH, blocks_of(g0) + off0, D, "mean0", &src0);
+    rows4(src1, B, NH, tokens_of(g1), D, "src1", &src0);
+    rows4(mean1, B, NH, blocks_of(g1) + off1, D, "mean1", &src0);
+  }
   const auto s0 = strides<4>(src0);
   const auto m0 = strides<4>(mean0);
   const auto s1 = strides<4>(src1);
@@ -132,6 +213,11 @@ void q_prep(const at::Tensor& src, at::Tensor& dst, at::Tensor& mean, c10::IntAr
   rank(mean, 4, "mean");
   c10::DeviceGuard guard(src.device());
   const li_tile_geom g = geom_of(geom);
+  const int64_t B = src.size(0), NH = src.size(1), D = src.size(3);
+  rows4(src, B, NH, tokens_of(g), D, "src");
+  tiles5(dst, B, NH, blocks_of(g), block_size_of(g), D, "dst", src);
+  TORCH_CHECK(dst.scalar_type() == src.scalar_type(), "dst must be ", src.scalar_type());
+  rows4(mean, B, NH, blocks_of(g), D, "mean", &src);
   const auto ss = strides<4>(src);
   const auto ds = strides<5>(dst);
   const auto ms = strides<4>(mean);
@@ -150,6 +236,16 @@ void kv_prep(const at::Tensor& k_src, const at::Tensor& v_src, at::Tensor& k_dst
   rank(k_mean, 4, "k_mean");
   c10::DeviceGuard guard(k_src.device());
   const li_tile_geom g = geom_of(geom);
+  {
+    const int64_t B = k_src.size(0), NH = k_src.size(1), D = k_src.size(3), nb = blocks_of(g);
+    rows4(k_src, B, NH, tokens_of(g), D, "k_src");
+    rows4(v_src, B, NH, tokens_of(g), D, "v_src", &k_src);
+    tiles5(k_dst, B, NH, nb + dst_off, block_size_of(g), D, "k_dst", k_src);
+    tiles5(v_dst, B, NH, nb + dst_off, block_size_of(g), D, "v_dst", k_src);
+    TORCH_CHECK(k_dst.scalar_type() == k_src.scalar_type() && v_dst.scalar_type() == k_src.scalar_type(),
+                "k_dst and v_dst must be ", k_src.scalar_type());
+    rows4(k_mean, B, NH, nb + pool_off, D, "k_mean", &k_src);
+  }
   const auto ks = strides<4>(k_src);
   const auto vs = strides<4>(v_src);
   const auto kd = strides<5>(k_dst);
@@ -167,6 +263,11 @@ void untile(const at::Tensor& src, at::Tensor& dst, c10::IntArrayRef geom) {
   rank(dst, 4, "dst");
   c10::DeviceGuard guard(src.device());
   const li_tile_geom g = geom_of(geom);
+  {
+    const int64_t B = dst.size(0), NH = dst.size(1), D = dst.size(3);
+    tiles5(src, B, NH, blocks_of(g), block_size_of(g), D, "src", src);
+    rows4(dst, B, NH, tokens_of(g), D, "dst", &src);
+  }
   const auto ss = strides<5>(src);
   const auto ds = strides<4>(dst);
   check("li_untile", li_untile(dtype_code(src), (int32_t)dst.size(0), (int32_t)dst.size(1), (int32_t)dst.size(3),
@@ -186,6 +287,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> block_mask(const at::Tensor& q_po
   c10::DeviceGuard guard(q_pool.device());
   const int64_t B = q_pool.size(0), NH = q_pool.size(1), nq = q_pool.size(2), D = q_pool.size(3);
   const int64_t nk = k_pool.size(2);
+  rows4(k_pool, B, NH, 0, D, "k_pool", &q_pool);
   auto iopt = q_pool.options().dtype(at::kInt);
   at::Tensor indices = at::empty({B, NH, nq, kmax}, iopt);
   at::Tensor counts = at::empty({B, NH, nq}, iopt);
@@ -209,6 +311,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> block_mask(const at::Tensor& q_po
   if (row_budget.has_value() && row_budget->defined()) {
     TORCH_CHECK(row_budget->scalar_type() == at::kInt && row_budget->is_contiguous() && row_budget->numel() == nq,
                 "row_budget must be a contiguous int32 tensor of ", nq, " entries");
+    on_device(q_pool, *row_budget, "row_budget");
     p.row_budget = row_budget->data_ptr<int32_t>();
   }
   p.scale = (float)(1.0 / std::sqrt((double)D));
@@ -241,6 +344,13 @@ at::Tensor bsa_fwd(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v
   const int64_t B = q.size(0), NH = q.size(1), Lq = q.size(2), D = q.size(3), Lk = k.size(2);
   TORCH_CHECK(out.is_contiguous() && out.sizes() == q.sizes() && out.scalar_type() == q.scalar_type(),
               "out must be a contiguous tensor of q's shape and dtype");
+  TORCH_CHECK(q.is_contiguous() && k.is_contiguous() && v.is_contiguous(), "q, k, v must be contiguous");
+  TORCH_CHECK(block_size > 0, "block_size must be positive");
+  rows4(k, B, NH, Lk, D, "k", &q);
+  TORCH_CHECK(v.sizes() == k.sizes(), "v must have k's shape ", k.sizes(), ", got ", v.sizes());
+  rows4(v, B, NH, Lk, D, "v", &q);
+  on_device(q, out, "out");
+  lists(indices, counts, B, NH, (Lq + block_size - 1) / block_size, q);
   at::Tensor lse = lse_or_empty(q, return_lse, B, NH, Lq);
   at::Tensor ws = workspace(q, B, NH, Lq, D, block_size, split || balance);
   const auto is = strides<4>(indices);
@@ -267,9 +377,16 @@ at::Tensor bsa_fwd_gather(const at::Tensor& q, const at::Tensor& k, const at::Te
   c10::DeviceGuard guard(q.device());
   const li_tile_geom gq = geom_of(q_geom), gk = geom_of(k_geom);
   const int64_t B = q.size(0), NH = q.size(1), D = q.size(3);
-  const int64_t nq = (int64_t)((gq.T + gq.tt - 1) / gq.tt) * gq.nh * gq.nw;
-  const int64_t bs = (int64_t)gq.tt * gq.th * gq.tw;
+  const int64_t nq = blocks_of(gq);
+  const int64_t bs = block_size_of(gq);
   rank(out, 4, "out");
+  rows4(q, B, NH, tokens_of(gq), D, "q");
+  rows4(k, B, NH, tokens_of(gk), D, "k", &q);
+  rows4(v, B, NH, tokens_of(gk), D, "v", &q);
+  rows4(out, B, NH, tokens_of(gq), D, "out", &q);
+  text(k_txt, num_txt_blk * bs, B, NH, D, "k_txt", q);
+  text(v_txt, num_txt_blk * bs, B, NH, D, "v_txt", q);
+  lists(indices, counts, B, NH, nq, q);
   at::Tensor lse = lse_or_empty(q, return_lse, B, NH, nq * bs);
   at::Tensor ws = workspace(q, B, NH, nq * bs, D, bs, split || balance);
   const at::Tensor kt = num_txt_blk > 0 && k_txt.has_value() ? *k_txt : at::Tensor();
@@ -301,6 +418,12 @@ at::Tensor attn_dense(const at::Tensor& q, const at::Tensor& k, const at::Tensor
   const int64_t B = q.size(0), NH = q.size(1), Lq = q.size(2), D = q.size(3), Lk = k.size(2);
   const int64_t nq = (Lq + 127) / 128;
   rank(out, 4, "out");
+  rows4(k, B, NH, Lk, D, "k", &q);
+  rows4(v, B, NH, Lk, D, "v", &q);
+  rows4(out, B, NH, Lq, D, "out", &q);
+  TORCH_CHECK(txt_len >= 0, "txt_len must be >= 0");
+  text(k_txt, (txt_len + 127) / 128 * 128, B, NH, D, "k_txt", q);
+  text(v_txt, (txt_len + 127) / 128 * 128, B, NH, D, "v_txt", q);
   at::Tensor lse = lse_or_empty(q, return_lse, B, NH, nq * 128);
   at::Tensor ws = workspace(q, B, NH, nq * 128, D, 128, split);
   const at::Tensor kt = txt_len > 0 && k_txt.has_value() ? *k_txt : at::Tensor();
@@ -327,6 +450,14 @@ void tile_prep_fp8(const at::Tensor& src, at::Tensor& dst, at::Tensor& scales, c
   c10::DeviceGuard guard(src.device());
   const li_tile_geom g = geom_of(geom);
   const at::Tensor m = mean.has_value() ? *mean : at::Tensor();
+  {
+    const int64_t B = src.size(0), NH = src.size(1), D = src.size(3), nb = blocks_of(g);
+    rows4(src, B, NH, tokens_of(g), D, "src");
+    tiles5(dst, B, NH, nb + dst_off, block_size_of(g), D, "dst", src);
+    codes(dst, "dst");
+    scales3(scales, B, NH, nb + dst_off, "scales", src);
+    if (m.defined()) rows4(m, B, NH, nb + pool_off, D, "mean", &src);
+  }
   const auto ss = strides<4>(src);
   const auto ds = strides<5>(dst);
   const auto cs = strides<3>(scales);
@@ -349,6 +480,17 @@ void kv_prep_fp8(const at::Tensor& k_src, const at::Tensor& v_src, at::Tensor& k
   rank(k_mean, 4, "k_mean");
   c10::DeviceGuard guard(k_src.device());
   const li_tile_geom g = geom_of(geom);
+  {
+    const int64_t B = k_src.size(0), NH = k_src.size(1), D = k_src.size(3), nb = blocks_of(g);
+    rows4(k_src, B, NH, tokens_of(g), D, "k_src");
+    rows4(v_src, B, NH, tokens_of(g), D, "v_src", &k_src);
+    tiles5(k_dst, B, NH, nb + dst_off, block_size_of(g), D, "k_dst", k_src);
+    codes(k_dst, "k_dst");
+    scales3(k_scales, B, NH, nb + dst_off, "k_scales", k_src);
+    tiles5(v_dst, B, NH, nb + dst_off, block_size_of(g), D, "v_dst", k_src);
+    TORCH_CHECK(v_dst.scalar_type() == k_src.scalar_type(), "v_dst must be ", k_src.scalar_type());
+    rows4(k_mean, B, NH, nb + pool_off, D, "k_mean", &k_src);
+  }
   const auto ks = strides<4>(k_src);
   const auto vs = strides<4>(v_src);
   const auto kd = strides<5>(k_dst);
@@ -377,6 +519,21 @@ at::Tensor bsa_fwd_fp8(const at::Tensor& q8, const at::Tensor& q_scale, const at
   TORCH_CHECK(out.is_contiguous() && out.dim() == 4 && out.size(0) == B && out.size(1) == NH && out.size(2) == Lq &&
                   out.size(3) == D && out.scalar_type() == at::kBFloat16,
               "out must be a contiguous bfloat16 tensor of q8's shape");
+  TORCH_CHECK(q8.is_contiguous() && k8.is_contiguous() && v.is_contiguous() && q_scale.is_contiguous() &&
+                  k_scale.is_contiguous(),
+              "q8, k8, v and the scales must be contiguous");
+  codes(q8, "q8");
+  codes(k8, "k8");
+  rows4(k8, B, NH, Lk, D, "k8");
+  rows4(v, B, NH, Lk, D, "v");
+  TORCH_CHECK(v.size(2) == Lk, "v must have k8's length ", Lk);
+  TORCH_CHECK(block_size > 0, "block_size must be positive");
+  scales3(q_scale, B, NH, (Lq + 127) / 128, "q_scale", q8);
+  scales3(k_scale, B, NH, Lk / 128, "k_scale", q8);
+  on_device(q8, k8, "k8");
+  on_device(q8, v, "v");
+  on_device(q8, out, "out");
+  lists(indices, counts, B, NH, (Lq + block_size - 1) / block_size, q8);
   at::Tensor lse = lse_or_empty(v, return_lse, B, NH, Lq);
   at::Tensor ws = workspace(v, B, NH, Lq, D, block_size, split || balance);
   const auto is = strides<4>(indices);
@@ -403,7 +560,23 @@ at::Tensor bsa_fwd_fp8_gather(const at::Tensor& q8, const at::Tensor& q_scale, c
   c10::DeviceGuard guard(q8.device());
   const li_tile_geom gq = geom_of(q_geom), gk = geom_of(k_geom);
   const int64_t B = v.size(0), NH = v.size(1), D = v.size(3);
-  const int64_t nq = (int64_t)((gq.T + gq.tt - 1) / gq.tt) * gq.nh * gq.nw;
+  const int64_t nq = blocks_of(gq);
+  TORCH_CHECK(block_size_of(gq) == 128, "the e4m3 gather path is built for 128-token tiles");
+  TORCH_CHECK(q8.is_contiguous() && k8.is_contiguous() && q_scale.is_contiguous() && k_scale.is_contiguous(),
+              "q8, k8 and the scales must be contiguous");
+  codes(q8, "q8");
+  codes(k8, "k8");
+  TORCH_CHECK(v.scalar_type() == at::kBFloat16, "v must be bfloat16");
+  rows4(q8, B, NH, nq * 128, D, "q8");
+  rows4(k8, B, NH, (num_txt_blk + blocks_of(gk)) * 128, D, "k8");
+  scales3(q_scale, B, NH, nq, "q_scale", v);
+  scales3(k_scale, B, NH, num_txt_blk + blocks_of(gk), "k_scale", v);
+  rows4(v, B, NH, tokens_of(gk), D, "v");
+  rows4(out, B, NH, tokens_of(gq), D, "out", &v);
+  on_device(v, q8, "q8");
+  on_device(v, k8, "k8");
+  text(v_txt, num_txt_blk * 128, B, NH, D, "v_txt", v);
+  lists(indices, counts, B, NH, nq, v);
   at::Tensor lse = lse_or_empty(v, return_lse, B, NH, nq * 128);
   at::Tensor ws = workspace(v, B, NH, nq * 128, D, 128, true);
   const at::Tensor vt = num_txt_blk > 0 && v_txt.has_value() ? *v_txt : at::Tensor();

@@ -90,3 +90,47 @@ def test_compiled_graph_calls_the_ops(dev):
     compiled = torch.compile(call, fullgraph=True, backend="aot_eager")(q, k, v)
     torch.cuda.synchronize()
     assert torch.equal(eager.view(torch.int16), compiled.view(torch.int16))
+
+
+def test_direct_calls_check_extents(dev):
+    """The operators reject tensors shorter than the geometry or lists index them, before any launch."""
+    print("[gpu] direct operator calls with short tensors raise", flush=True)
+    q, k, v = _tokens(dev, seed=10), _tokens(dev, frames=4, seed=11), _tokens(dev, frames=4, seed=12)
+    gq, gk = [2, 16, 16, 2, 8, 8, 2, 2], [4, 16, 16, 2, 8, 8, 2, 2]
+    short_k = k[:, :, :-1]
+    qp = torch.zeros((1, 2, 4, 128), dtype=torch.bfloat16, device=dev)
+    kp = torch.zeros((1, 2, 8, 128), dtype=torch.bfloat16, device=dev)
+    ind, cnt = _lists(dev, 2, 4, 8, 5)
+    scale = 1.0 / math.sqrt(128)
+    cases = [
+        ("src must", lambda: torch.ops.li.pool(short_k, kp, 0, gk)),
+        ("mean must", lambda: torch.ops.li.pool(k, kp[:, :, :7], 0, gk)),
+        ("mean must", lambda: torch.ops.li.pool(k, kp, 1, gk)),
+        ("src1 must", lambda: torch.ops.li.pool_pair(q, qp, 0, gq, short_k, kp, 0, gk)),
+        ("dst must", lambda: torch.ops.li.q_prep(q, torch.empty((1, 2, 3, 128, 128), dtype=torch.bfloat16, device=dev),
+                                            qp, gq)),
+        ("dst must", lambda: torch.ops.li.untile(torch.empty((1, 2, 4, 128, 128), dtype=torch.bfloat16, device=dev),
+                                            q[:, :, :-1], gq)),
+        ("k_pool must", lambda: torch.ops.li.block_mask(qp, kp[..., :64], 1, 0, 0.5, 7, 0, True, True, False, 2, 2, 0, 8,
+                                                   None, False)),
+        ("k must", lambda: torch.ops.li.bsa_fwd_gather(q, short_k, v, None, None, 0, gq, gk, ind, cnt, scale,
+                                                  torch.empty_like(q), False, True, False)),
+        ("block_indices must", lambda: torch.ops.li.bsa_fwd_gather(q, k, v, None, None, 0, gq, gk, ind[:, :, :3], cnt,
+                                                              scale, torch.empty_like(q), False, True, False)),
+        ("k_txt is required", lambda: torch.ops.li.bsa_fwd_gather(q, k, v, None, None, 1, gq, gk, ind, cnt, scale,
+                                                      torch.empty_like(q), False, True, False)),
+        ("block_counts must", lambda: torch.ops.li.bsa_fwd(q.contiguous(), k.contiguous(), v.contiguous(), ind,
+                                                      cnt[:, :, :2], scale, 128, torch.empty_like(q.contiguous()),
+                                                      False, True, False)),
+        ("v must", lambda: torch.ops.li.attn_dense(q, k, v[:, :, :-128], None, None, 0, scale, torch.empty_like(q),
+                                              False, True)),
+    ]
+    for what, call in cases:
+        with pytest.raises(RuntimeError, match=what):
+            call()
+    torch.cuda.synchronize()
+    # The valid calls still run.
+    torch.ops.li.pool_pair(q, qp, 0, gq, k, kp, 0, gk)
+    torch.ops.li.bsa_fwd_gather(q, k, v, None, None, 0, gq, gk, ind, cnt, scale, torch.empty_like(q), False, True,
+                                False)
+    torch.cuda.synchronize()
