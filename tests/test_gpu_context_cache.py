@@ -67,6 +67,35 @@ def test_cached_calls_give_the_uncached_bits(dev, fused, fp8, text):
     assert len(cache) == 0
 
 
+@pytest.mark.parametrize("text", [0, 200])
+def test_cached_cosine_calls_with_the_normalised_key_pool(dev, text):
+    """Cosine selection: the key pool's normalised copy is cached with the pool and kept in step with it."""
+    print(f"[gpu] context cache, cosine selection through the normalised key pool, text={text}", flush=True)
+    wl = _wl()
+    params = dict(wl.sparse_params(), tile_size=wl.tile, sim_metric="cosine")
+
+    def select(q_pool, k_pool, tl, grid_q, grid_k):
+        return fast_generate_indices(q_pool, k_pool, tl, grid_q, grid_k, params, dev)
+
+    def call(q, k, v, kt, vt, context, norm):
+        return _pipeline.sparse_attention(q, kt, vt, k, v, wl.latent_hw, wl.tile, select, context=context,
+                                          normalize_k_pool=norm)
+
+    q, k, v, kt, vt = _inputs(dev, 3, text)
+    cache = ContextCache()
+    ref1 = call(q, k, v, kt, vt, None, False)             # the mask normalises the raw pool itself
+    out1 = call(q, k, v, kt, vt, (cache, 2, 8), True)     # fills the cache (pool + normalised copy)
+    q2, k2, v2 = _new_chunk(q, k, v, 4)
+    ref2 = call(q2, k2, v2, kt, vt, None, False)
+    out2 = call(q2, k2, v2, kt, vt, (cache, 2, 8), True)  # context rows of both from the cache
+    raw2 = call(q2, k2, v2, kt, vt, (cache, 2, 8), False)  # a raw-pool entry of its own
+    torch.cuda.synchronize()
+    assert len(cache) == 2
+    for out, ref in ((out1, ref1), (out2, ref2), (raw2, ref2)):
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    assert not torch.equal(ref1, ref2)
+
+
 def test_entry_point_keys_and_layers(dev):
     """Through run_sparse_attention: one entry per layer (block_idx); an odd context is rounded down to whole slabs."""
     print("[gpu] context cache through run_sparse_attention", flush=True)
