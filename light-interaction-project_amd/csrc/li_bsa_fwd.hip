@@ -1557,7 +1557,10 @@ bool row_view_ok(const void* p, const int64_t st[4]) {
 // array, zero from module load and never written.  Each device holds its own
 // copy until the process ends; host code passes zero_region_ptr(), never the
 // array's name.
-constexpr int64_t kZeroRegionBytes = 64ll << 20;
+// 32 MiB reaches the largest row offset of the call shapes of both models
+// (HY-WorldPlay's (4, 8, 4) tile over a 30 x 52 grid: 5047 tokens of up to
+// 24 heads x 128 bf16 = 31 MB); larger calls pick their sources per chunk.
+constexpr int64_t kZeroRegionBytes = 32ll << 20;
 static __device__ __align__(256) char g_zero_region[kZeroRegionBytes];
 
 namespace {

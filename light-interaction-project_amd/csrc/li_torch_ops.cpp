@@ -101,11 +101,16 @@ void on_device(const at::Tensor& ref, const at::Tensor& t, const char* name) {
   TORCH_CHECK(t.device() == ref.device(), name, " must be on ", ref.device(), ", got ", t.device());
 }
 
-// (B, NH, >= rows, D), with the element type of `like` when given.
+// (B, NH, >= rows, D), with the element type of `like` when given.  With
+// `exact`, exactly `rows` rows: for contiguous tensors that a kernel indexes at
+// a per-head pitch implied by the geometry rather than by a stride, where a
+// longer tensor would make every head after the first read another head's
+// rows.
 void rows4(const at::Tensor& t, int64_t B, int64_t NH, int64_t rows, int64_t D, const char* name,
-           const at::Tensor* like = nullptr) {
-  TORCH_CHECK(t.dim() == 4 && t.size(0) == B && t.size(1) == NH && t.size(2) >= rows && t.size(3) == D, name,
-              " must be (", B, ", ", NH, ", >= ", rows, ", ", D, "), got ", t.sizes());
+           const at::Tensor* like = nullptr, bool exact = false) {
+  TORCH_CHECK(t.dim() == 4 && t.size(0) == B && t.size(1) == NH && (exact ? t.size(2) == rows : t.size(2) >= rows) &&
+                  t.size(3) == D,
+              name, " must be (", B, ", ", NH, ", ", exact ? "" : ">= ", rows, ", ", D, "), got ", t.sizes());
   if (like) {
     on_device(*like, t, name);
     TORCH_CHECK(t.scalar_type() == like->scalar_type(), name, " must be ", like->scalar_type(), ", got ",
@@ -122,11 +127,13 @@ void tiles5(const at::Tensor& t, int64_t B, int64_t NH, int64_t blocks, int64_t 
   on_device(ref, t, name);
 }
 
-// (B, NH, >= blocks) fp32 scales.
-void scales3(const at::Tensor& t, int64_t B, int64_t NH, int64_t blocks, const char* name, const at::Tensor& ref) {
-  TORCH_CHECK(t.dim() == 3 && t.size(0) == B && t.size(1) == NH && t.size(2) >= blocks &&
-                  t.scalar_type() == at::kFloat,
-              name, " must be float32 (", B, ", ", NH, ", >= ", blocks, "), got ", t.scalar_type(), " ", t.sizes());
+// (B, NH, >= blocks) fp32 scales; exactly `blocks` with `exact` (as for rows4).
+void scales3(const at::Tensor& t, int64_t B, int64_t NH, int64_t blocks, const char* name, const at::Tensor& ref,
+             bool exact = false) {
+  TORCH_CHECK(t.dim() == 3 && t.size(0) == B && t.size(1) == NH &&
+                  (exact ? t.size(2) == blocks : t.size(2) >= blocks) && t.scalar_type() == at::kFloat,
+              name, " must be float32 (", B, ", ", NH, ", ", exact ? "" : ">= ", blocks, "), got ", t.scalar_type(),
+              " ", t.sizes());
   on_device(ref, t, name);
 }
 
@@ -145,13 +152,14 @@ void lists(const at::Tensor& indices, const at::Tensor& counts, int64_t B, int64
   on_device(ref, counts, "block_counts");
 }
 
-// Contiguous text rows (B, NH, >= rows, D) when there are any.
+// Contiguous zero-padded text rows, exactly (B, NH, rows, D), when there are
+// any: the kernels index them at a per-head pitch of `rows` rows.
 void text(const c10::optional<at::Tensor>& t, int64_t rows, int64_t B, int64_t NH, int64_t D, const char* name,
           const at::Tensor& like) {
   if (rows <= 0) return;
   TORCH_CHECK(t.has_value() && t->defined(), name, " is required with text blocks");
   TORCH_CHECK(t->is_contiguous(), name, " must be contiguous");
-  rows4(*t, B, NH, rows, D, name, &like);
+  rows4(*t, B, NH, rows, D, name, &like, true);
 }
 
 // ---------------------------------------------------------------------------
@@ -528,8 +536,10 @@ at::Tensor bsa_fwd_fp8(const at::Tensor& q8, const at::Tensor& q_scale, const at
   rows4(v, B, NH, Lk, D, "v");
   TORCH_CHECK(v.size(2) == Lk, "v must have k8's length ", Lk);
   TORCH_CHECK(block_size > 0, "block_size must be positive");
-  scales3(q_scale, B, NH, (Lq + 127) / 128, "q_scale", q8);
-  scales3(k_scale, B, NH, Lk / 128, "k_scale", q8);
+  // One scale per block of block_size rows (the library takes 128 only),
+  // indexed at per-head pitches of the tile and block counts.
+  scales3(q_scale, B, NH, (Lq + block_size - 1) / block_size, "q_scale", q8, true);
+  scales3(k_scale, B, NH, Lk / block_size, "k_scale", q8, true);
   on_device(q8, k8, "k8");
   on_device(q8, v, "v");
   on_device(q8, out, "out");
@@ -567,10 +577,12 @@ at::Tensor bsa_fwd_fp8_gather(const at::Tensor& q8, const at::Tensor& q_scale, c
   codes(q8, "q8");
   codes(k8, "k8");
   TORCH_CHECK(v.scalar_type() == at::kBFloat16, "v must be bfloat16");
-  rows4(q8, B, NH, nq * 128, D, "q8");
-  rows4(k8, B, NH, (num_txt_blk + blocks_of(gk)) * 128, D, "k8");
-  scales3(q_scale, B, NH, nq, "q_scale", v);
-  scales3(k_scale, B, NH, num_txt_blk + blocks_of(gk), "k_scale", v);
+  // Tiles and scales are indexed at per-head pitches of the geometry's block
+  // counts: exact extents.
+  rows4(q8, B, NH, nq * 128, D, "q8", nullptr, true);
+  rows4(k8, B, NH, (num_txt_blk + blocks_of(gk)) * 128, D, "k8", nullptr, true);
+  scales3(q_scale, B, NH, nq, "q_scale", v, true);
+  scales3(k_scale, B, NH, num_txt_blk + blocks_of(gk), "k_scale", v, true);
   rows4(v, B, NH, tokens_of(gk), D, "v");
   rows4(out, B, NH, tokens_of(gq), D, "out", &v);
   on_device(v, q8, "q8");

@@ -199,14 +199,6 @@ def pool_pair(src0, mean0, pool_off0, geom0, src1, mean1, pool_off1, geom1, mean
     _run(ops.pool_pair, src0, mean0, int(pool_off0), gs[0], src1, mean1, int(pool_off1), gs[1], mean1_normalized)
 
 
-def attach_normalized(k_pool, k_pool_normalized):
-    """Mark ``k_pool_normalized`` as ``k_pool`` with every row normalised for the cosine metric (as
-    ``pool_pair``'s ``mean1_normalized`` writes it); ``block_mask`` with ``metric="cosine"`` then scores
-    against it instead of normalising every key row once per workgroup of query rows (same bits).  The
-    writer of ``k_pool`` keeps the two in step."""
-    k_pool.li_normalized = k_pool_normalized
-
-
 def fused_supported(D, tile, latent_hw):
     """Whether li_bsa_fwd_gather covers this shape.
 
@@ -244,6 +236,9 @@ def bsa_forward_gather(q, k, v, k_txt, v_txt, num_txt_blk, T_q, T_k, H, W, tt, t
         _same_dtype(q, k_txt, v_txt)
         if not (k_txt.is_contiguous() and v_txt.is_contiguous()):
             raise ValueError("padded text K/V must be contiguous")
+        want = (B, NH, num_txt_blk * tt * th * tw, D)
+        if tuple(k_txt.shape) != want or tuple(v_txt.shape) != want:
+            raise ValueError(f"padded text K/V must be {want}, got {tuple(k_txt.shape)} / {tuple(v_txt.shape)}")
     dtype_code(q)
     lse = _run(ops.bsa_fwd_gather, q, k, v, k_txt if num_txt_blk > 0 else None,
                v_txt if num_txt_blk > 0 else None, int(num_txt_blk), [T_q, H, W, tt, th, tw, nh, nw],
@@ -375,12 +370,14 @@ def _mask_plan(dev, nq, nk, nh, nw, num_txt_blk, n_recent, force_diag, force_sin
 
 def block_mask(q_pool, k_pool, *, metric, budget_mode, ratio, nh, nw, num_txt_blk=0, n_recent=0,
                force_diag=False, force_sink=False, force_neighbors=False, min_budget=7, row_budget=None,
-               return_scores=False):
+               return_scores=False, k_pool_normalized=None):
     """Block selection on the device (see li_block_mask).
 
     Returns ``(indices (B,H,nq,kmax) int32, counts (B,H,nq) int32)`` (+ scores if asked), where
-    ``kmax = num_txt_blk + max row budget``.  With ``metric="cosine"``, a ``k_pool`` that carries its
-    normalised copy (``attach_normalized``) is scored through that copy.
+    ``kmax = num_txt_blk + max row budget``.  ``k_pool_normalized``: ``k_pool`` with every row normalised
+    for the cosine metric, as ``pool_pair``'s ``mean1_normalized`` writes it in the same launch as the
+    pool; with ``metric="cosine"`` the mask scores against it instead of normalising every key row once
+    per workgroup of query rows (same bits).  Other metrics ignore it.  The caller keeps the two in step.
     """
     dev = _device_check(q_pool, k_pool)
     _same_dtype(q_pool, k_pool)
@@ -392,7 +389,7 @@ def block_mask(q_pool, k_pool, *, metric, budget_mode, ratio, nh, nw, num_txt_bl
     kmax, rb_dev = _mask_plan(dev, nq, nk, nh, nw, num_txt_blk, n_recent, bool(force_diag), bool(force_sink),
                               bool(force_neighbors), budget_mode, float(ratio), int(min_budget), row_budget)
     dtype_code(q_pool)
-    k_norm = getattr(k_pool, "li_normalized", None) if metric_code == _lib.LI_METRIC_COSINE else None
+    k_norm = k_pool_normalized if metric_code == _lib.LI_METRIC_COSINE else None
     if k_norm is not None:
         if k_norm.shape != k_pool.shape or k_norm.dtype != k_pool.dtype or k_norm.device != k_pool.device:
             raise ValueError("the normalised key pool does not match the key pool")

@@ -50,6 +50,22 @@ def _nblk(geom):
     return -(-T // tt) * nh * nw
 
 
+def _exact(t, shape, name):
+    """The checks of the operator library for tensors its kernels index at a per-head pitch implied by the
+    geometry (contiguous padded text K/V, e4m3 tiles and scales): exactly ``shape``, so that a longer tensor
+    cannot make heads after the first read another head's rows."""
+    if t is not None and tuple(t.shape) != tuple(shape):
+        raise RuntimeError(f"{name} must be {tuple(shape)}, got {tuple(t.shape)}")
+
+
+def _text(t, rows, like, name):
+    if rows > 0:
+        if t is None:
+            raise RuntimeError(f"{name} is required with text blocks")
+        B, NH, _, D = like.shape
+        _exact(t, (B, NH, rows, D), name)
+
+
 @torch.library.register_fake("li::pool")
 def _pool_fake(src, mean, pool_off, geom):
     return None
@@ -97,12 +113,16 @@ def _bsa_fwd_gather_fake(q, k, v, k_txt, v_txt, num_txt_blk, q_geom, k_geom, ind
                          return_lse, split, balance, sorted=False):
     B, NH = q.shape[:2]
     bs = q_geom[3] * q_geom[4] * q_geom[5]
+    _text(k_txt, num_txt_blk * bs, q, "k_txt")
+    _text(v_txt, num_txt_blk * bs, q, "v_txt")
     return _lse(q, return_lse, B, NH, _nblk(q_geom) * bs)
 
 
 @torch.library.register_fake("li::attn_dense")
 def _attn_dense_fake(q, k, v, k_txt, v_txt, txt_len, sm_scale, out, return_lse, split):
     B, NH, Lq, _ = q.shape
+    _text(k_txt, -(-txt_len // 128) * 128, q, "k_txt")
+    _text(v_txt, -(-txt_len // 128) * 128, q, "v_txt")
     return _lse(q, return_lse, B, NH, -(-Lq // 128) * 128)
 
 
@@ -120,11 +140,19 @@ def _kv_prep_fp8_fake(k_src, v_src, k_dst, k_scales, v_dst, k_mean, dst_off, poo
 def _bsa_fwd_fp8_fake(q8, q_scale, k8, k_scale, v, indices, counts, sm_scale, block_size, out, return_lse, split,
                       balance):
     B, NH, Lq, _ = q8.shape
+    _exact(q_scale, (B, NH, -(-Lq // block_size)), "q_scale")
+    _exact(k_scale, (B, NH, k8.shape[2] // block_size), "k_scale")
     return _lse(v, return_lse, B, NH, Lq)
 
 
 @torch.library.register_fake("li::bsa_fwd_fp8_gather")
 def _bsa_fwd_fp8_gather_fake(q8, q_scale, k8, k_scale, v, v_txt, num_txt_blk, q_geom, k_geom, indices, counts,
                              sm_scale, out, return_lse, balance, sorted=False):
-    B, NH = v.shape[:2]
-    return _lse(v, return_lse, B, NH, _nblk(q_geom) * 128)
+    B, NH, _, D = v.shape
+    nq, nkb = _nblk(q_geom), num_txt_blk + _nblk(k_geom)
+    _exact(q8, (B, NH, nq * 128, D), "q8")
+    _exact(k8, (B, NH, nkb * 128, D), "k8")
+    _exact(q_scale, (B, NH, nq), "q_scale")
+    _exact(k_scale, (B, NH, nkb), "k_scale")
+    _text(v_txt, num_txt_blk * 128, v, "v_txt")
+    return _lse(v, return_lse, B, NH, nq * 128)

@@ -139,7 +139,7 @@ def _k_side(path, k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, d
     q_pool_job: (q, q_pool, pool_off, geometry) of the query pool, taken in the same launch as the K pool on
     the fused path (li_pool_pair), or on its own when there is no K pool to take (every frame cached).
     k_norm: on the fused path, also keep the K pool's rows normalised for the cosine selection (written by
-    the same launch and attached to the K pool, see _core.attach_normalized).
+    the same launch, ``k_pool_n``; the selection takes it as ``k_pool_normalized``).
     """
     cache, layer, cframes = ctx if ctx is not None else (None, None, 0)
     cf = min((max(cframes, 0) // g.tt) * g.tt, g.T_k) if cache is not None else 0
@@ -152,7 +152,6 @@ def _k_side(path, k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, d
         bufs = {"k_pool": torch.empty((B, NH, g.nk_blk, D), device=dev, dtype=dt), "k_pool_n": None}
         if k_norm:
             bufs["k_pool_n"] = torch.empty_like(bufs["k_pool"])
-            _core.attach_normalized(bufs["k_pool"], bufs["k_pool_n"])
         if path in ("fused_fp8", "tiled_fp8"):
             bufs["k8"] = torch.empty((B, NH, nkb, g.bs, D), device=dev, dtype=_core.FP8)
             bufs["k_scale"] = torch.empty((B, NH, nkb), device=dev, dtype=torch.float32)
@@ -203,7 +202,14 @@ def _k_side(path, k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, d
     return bufs
 
 
-def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance, ctx, k_norm=False):
+def _select(select, q_pool, kb, text_len, g):
+    """``select`` on the call's pools; the normalised key pool goes along only when the call wrote one."""
+    kw = {} if kb.get("k_pool_n") is None else {"k_pool_normalized": kb["k_pool_n"]}
+    return select(q_pool, kb["k_pool"], text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw), **kw)
+
+
+def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance, ctx, sorted_lists,
+           k_norm=False):
     """Pools, block selection, then one kernel that gathers, attends and untiles."""
     B, NH, _, D = q.shape
     dev, dt = q.device, q.dtype
@@ -217,12 +223,12 @@ def _fused(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events
                  k_norm=k_norm)
     _stage(events, "prep_end")
     _stage(events, "index_start")
-    indices, counts = select(q_pool, kb["k_pool"], text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
+    indices, counts = _select(select, q_pool, kb, text_len, g)
     _stage(events, "index_end")
     _stage(events, "attn_start")
     _core.bsa_forward_gather(q, k_vis, v_vis, kb["kt"], kb["vt"], g.num_txt_blk, g.T_q, g.T_k, g.H, g.W, g.tt, g.th,
                              g.tw, g.nh, g.nw, indices, counts, 1.0 / math.sqrt(D), o_out, balance=balance,
-                             sorted_lists=True)
+                             sorted_lists=sorted_lists)
     _stage(events, "attn_end")
     _stage(events, "untile_start")
     _stage(events, "untile_end")
@@ -242,7 +248,7 @@ def _q_fp8(q, g, B, NH, D, dev):
     return q8, q_scale, q_pool
 
 
-def _tiled_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance, ctx):
+def _tiled_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance, ctx, sorted_lists):
     """Tiled sequence with Q and K quantized to e4m3 per tile block (scale amax / 448) in their gathers.
 
     The pools (and so the block selection) are those of the bf16 path; V, P V and the output stay bf16.
@@ -256,7 +262,7 @@ def _tiled_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, ev
     kb = _k_side("tiled_fp8", k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, q.dtype)
     _stage(events, "prep_end")
     _stage(events, "index_start")
-    indices, counts = select(q_pool, kb["k_pool"], text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
+    indices, counts = _select(select, q_pool, kb, text_len, g)
     _stage(events, "index_end")
     _stage(events, "attn_start")
     o_flat = _core.bsa_forward_fp8(q8.flatten(2, 3), q_scale, kb["k8"].flatten(2, 3), kb["k_scale"],
@@ -270,7 +276,7 @@ def _tiled_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, ev
     return o_out if o_out.dtype == out_dtype else o_out.to(out_dtype)
 
 
-def _fused_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance, ctx):
+def _fused_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance, ctx, sorted_lists):
     """e4m3 Q/K tiles from the quantizing gathers, then one kernel that reads V and writes O in token order."""
     B, NH, _, D = q.shape
     dev = q.device
@@ -282,12 +288,12 @@ def _fused_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, ev
     kb = _k_side("fused_fp8", k_txt, v_txt, k_vis, v_vis, g, text_len, ctx, B, NH, D, dev, q.dtype)
     _stage(events, "prep_end")
     _stage(events, "index_start")
-    indices, counts = select(q_pool, kb["k_pool"], text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
+    indices, counts = _select(select, q_pool, kb, text_len, g)
     _stage(events, "index_end")
     _stage(events, "attn_start")
     _core.bsa_forward_fp8_gather(q8.flatten(2, 3), q_scale, kb["k8"].flatten(2, 3), kb["k_scale"], v_vis, kb["vt"],
                                  g.num_txt_blk, g.T_q, g.T_k, g.H, g.W, g.tt, g.th, g.tw, g.nh, g.nw, indices, counts,
-                                 1.0 / math.sqrt(D), o_out, balance=balance, sorted_lists=True)
+                                 1.0 / math.sqrt(D), o_out, balance=balance, sorted_lists=sorted_lists)
     _stage(events, "attn_end")
     _stage(events, "untile_start")
     _stage(events, "untile_end")
@@ -295,13 +301,14 @@ def _fused_fp8(q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, ev
 
 
 def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, events=None, fused=True,
-                     balance=False, qk_fp8=False, context=None, normalize_k_pool=False):
+                     balance=False, qk_fp8=False, context=None, normalize_k_pool=False, sorted_lists=False):
     """One sparse-attention forward.
 
     q (B,H,Lq,D); k_txt/v_txt (B,H,N_txt,D) or None; k_vis/v_vis (B,H,Lk,D), any strides.
-    ``select(q_pool, k_pool, text_len, grid_q, grid_k) -> (indices, counts)``, with every row listing its
-    text blocks before its visual blocks, as the block mask's ascending lists do (the fused kernels take
-    their faster load path on that basis).
+    ``select(q_pool, k_pool, text_len, grid_q, grid_k) -> (indices, counts)``.  ``sorted_lists``: every
+    row ``select`` returns lists its text blocks before its visual blocks, as the block mask's ascending
+    lists do; the token-order kernels then take their faster load path (a text block listed after a
+    visual block would read as zeros, so leave it off for other selectors).
     ``events`` (dict or None) collects CUDA events per stage for profiling.
     ``fused`` (default) runs pools + one gather/attend/untile kernel where the
     shape allows it (D = 128, 128-token tiles, tw and W multiples of 4, a grid
@@ -314,7 +321,8 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
     fixed leading frames and the text across calls (see ContextCache).  ``normalize_k_pool`` (``select``
     scores by cosine similarity): the fused bf16/f16 path's pool launch also writes the key pool's rows
     normalised, once per key block, and the block mask takes them instead of normalising every key row in
-    every workgroup of query rows (same selection, bit for bit).
+    every workgroup of query rows (same selection, bit for bit); ``select`` then receives it as the
+    keyword argument ``k_pool_normalized``.
     """
     out_dtype = q.dtype
     if q.dtype not in (torch.bfloat16, torch.float16):
@@ -325,7 +333,7 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
     g = geometry(latent_hw, tile, q.shape[2], k_vis.shape[2], text_len)
     B, NH, _, D = q.shape
     dev, dt = q.device, q.dtype
-    args = (q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance, context)
+    args = (q, k_txt, v_txt, k_vis, v_vis, g, select, text_len, out_dtype, events, balance, context, sorted_lists)
     if qk_fp8:
         if dt != torch.bfloat16 or not fp8_supported(D, tile):
             raise ValueError(f"qk_fp8 is built for bfloat16, D = 128 and 128-token tiles (got {dt}, D = {D}, "
@@ -344,7 +352,7 @@ def sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, eve
     kb = _k_side("tiled", k_txt, v_txt, k_vis, v_vis, g, text_len, context, B, NH, D, dev, dt)
     _stage(events, "prep_end")
     _stage(events, "index_start")
-    indices, counts = select(q_pool, kb["k_pool"], text_len, (g.nt_q, g.nh, g.nw), (g.nt_k, g.nh, g.nw))
+    indices, counts = _select(select, q_pool, kb, text_len, g)
     _stage(events, "index_end")
     _stage(events, "attn_start")
     o_flat = _core.bsa_forward(q_tiled.flatten(2, 3), kb["k_all"].flatten(2, 3), kb["v_all"].flatten(2, 3), indices,

@@ -28,11 +28,13 @@ def launch_untile(src, dst, T, H, W, tt, th, tw, nh, nw):
     _core.untile(src, dst, T, H, W, tt, th, tw, nh, nw)
 
 
-def fast_generate_indices(q_pool, k_pool, text_len, grid_thw_q, grid_thw_k, params, device):
+def fast_generate_indices(q_pool, k_pool, text_len, grid_thw_q, grid_thw_k, params, device, *,
+                          k_pool_normalized=None):
     """Block-sparse indices for the AR decode path (ar_sparse_operation.py:223-284).
 
     Returns ``(final_indices (B, H, Nq_blk, K) int32, final_counts (B, H, Nq_blk) int32)``:
-    text blocks first, then the selected visual blocks ascending.
+    text blocks first, then the selected visual blocks ascending.  ``k_pool_normalized`` (extension,
+    keyword only): the key pool's rows normalised for the cosine metric, see ``_core.block_mask``.
     """
     tt, th, tw = params["tile_size"]
     bs = tt * th * tw
@@ -42,7 +44,8 @@ def fast_generate_indices(q_pool, k_pool, text_len, grid_thw_q, grid_thw_k, para
     num_txt_blk = (text_len + bs - 1) // bs
     return _core.block_mask(q_pool, k_pool, metric=params.get("sim_metric", "cosine"),
                             budget_mode=_lib.LI_BUDGET_HISTORY, ratio=params.get("topk_ratio", 1.0), nh=nh, nw=nw,
-                            num_txt_blk=num_txt_blk, n_recent=n_prot, **_pipeline.extras(params))
+                            num_txt_blk=num_txt_blk, n_recent=n_prot, k_pool_normalized=k_pool_normalized,
+                            **_pipeline.extras(params))
 
 
 def run_sparse_attention(q, k_txt, v_txt, k_vis, v_vis, block_idx, latent_hw, sparse_params):
@@ -62,11 +65,12 @@ def run_sparse_attention(q, k_txt, v_txt, k_vis, v_vis, block_idx, latent_hw, sp
         return _pipeline.dense_attention(q, k_txt, v_txt, k_vis, v_vis)
     tile = tuple(sparse_params.get("tile_size", (4, 8, 4)))
 
-    def select(q_pool, k_pool, text_len, grid_q, grid_k):
+    def select(q_pool, k_pool, text_len, grid_q, grid_k, k_pool_normalized=None):
         return fast_generate_indices(q_pool, k_pool, text_len, grid_q, grid_k, dict(sparse_params, tile_size=tile),
-                                     q.device)
+                                     q.device, k_pool_normalized=k_pool_normalized)
 
-    return _pipeline.sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select,
+    # The block mask lists every row's text blocks first (ascending ids).
+    return _pipeline.sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, sorted_lists=True,
                                       balance=_pipeline.ragged(sparse_params),
                                       qk_fp8=_pipeline.qk_fp8(sparse_params),
                                       context=_pipeline.context_of(sparse_params, block_idx),

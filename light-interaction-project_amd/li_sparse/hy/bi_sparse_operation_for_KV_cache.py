@@ -17,13 +17,16 @@ def _pool(x):
     return x.mean(dim=-2) if x.dim() == 5 else x
 
 
-def generate_prefill_indices(q_in, k_in, text_len, grid_thw, params, device, default_ratio=None):
+def generate_prefill_indices(q_in, k_in, text_len, grid_thw, params, device, default_ratio=None, *,
+                             k_pool_normalized=None):
     """Block-sparse indices for the bidirectional prefill phase.
 
     ``q_in`` / ``k_in`` are pooled ``(B, H, N, D)`` or tiled ``(B, H, N, Bs, D)``
     (mean-pooled here, bi_sparse_operation_for_KV_cache.py:239-250).  Key blocks
     at 3D Manhattan distance <= 1 from the query's block are always kept.
-    ``params['topk_ratio']`` is required (``default_ratio`` is the MG entry's 0.25).
+    ``params['topk_ratio']`` is required (``default_ratio`` is the MG entry's 0.25).  ``k_pool_normalized``
+    (extension, keyword only, pooled ``k_in`` only): the key pool's rows normalised for the cosine metric,
+    see ``_core.block_mask``.
     """
     if q_in.dim() == 5:
         bs = q_in.shape[-2]
@@ -36,7 +39,9 @@ def generate_prefill_indices(q_in, k_in, text_len, grid_thw, params, device, def
     num_txt_blk = (text_len + bs - 1) // bs
     return _core.block_mask(q_pool, k_pool, metric=params.get("sim_metric", "cosine"),
                             budget_mode=_lib.LI_BUDGET_TOTAL, ratio=ratio, nh=nh, nw=nw, num_txt_blk=num_txt_blk,
-                            force_neighbors=True, min_budget=7, **_pipeline.extras(params))
+                            force_neighbors=True, min_budget=7,
+                            k_pool_normalized=k_pool_normalized if k_in.dim() == 4 else None,
+                            **_pipeline.extras(params))
 
 
 def run_sparse_prefill_attention(q, k_txt, v_txt, k_vis, v_vis, block_idx, latent_hw, sparse_params):
@@ -47,11 +52,12 @@ def run_sparse_prefill_attention(q, k_txt, v_txt, k_vis, v_vis, block_idx, laten
         return _pipeline.dense_attention(q, k_txt, v_txt, k_vis, v_vis)
     tile = tuple(sparse_params.get("tile_size", (4, 8, 4)))
 
-    def select(q_pool, k_pool, text_len, grid_q, grid_k):
+    def select(q_pool, k_pool, text_len, grid_q, grid_k, k_pool_normalized=None):
         return generate_prefill_indices(q_pool, k_pool, text_len, grid_k, dict(sparse_params, tile_size=tile),
-                                        q.device)
+                                        q.device, k_pool_normalized=k_pool_normalized)
 
-    return _pipeline.sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select,
+    # The block mask lists every row's text blocks first (ascending ids).
+    return _pipeline.sparse_attention(q, k_txt, v_txt, k_vis, v_vis, latent_hw, tile, select, sorted_lists=True,
                                       balance=_pipeline.ragged(sparse_params),
                                       qk_fp8=_pipeline.qk_fp8(sparse_params),
                                       context=_pipeline.context_of(sparse_params, block_idx),

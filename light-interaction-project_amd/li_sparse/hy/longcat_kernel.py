@@ -12,7 +12,8 @@ _HALF = (torch.float16, torch.bfloat16)
 
 
 def _prepare(q, k, v):
-    # Non-half inputs are computed in bf16 (matrix-game-3.0 longcat_kernel.py:139-147).
+    # Non-half inputs are computed in bf16 (matrix-game-3.0 longcat_kernel.py:139-147);
+    # K and V follow Q's (possibly cast) dtype, since the kernels take one element type.
     q = q if q.dtype in _HALF else q.to(torch.bfloat16)
     k = k.to(q.dtype) if k.dtype != q.dtype else k
     v = v.to(q.dtype) if v.dtype != q.dtype else v
@@ -32,12 +33,15 @@ def longcat_flash_attn(q, k, v, block_indices, block_counts, sm_scale=None, logi
         logical_block_size: key block size, also the query tile size (64 or 128).
 
     Returns:
-        Attention output ``(B, H, Q_len, D)``.
+        Attention output ``(B, H, Q_len, D)`` in q's dtype, as ``torch.empty_like(q)``
+        gives it in the reference (longcat_kernel.py:198); a float32 (or other
+        non-half) q is computed in bf16 and the output cast back.
 
     Raises:
         ValueError: if K_len is not divisible by logical_block_size or a block
         index is out of bounds (checked on the host, as the reference does).
     """
+    out_dtype = q.dtype
     q, k, v = _prepare(q, k, v)
     block_indices = block_indices.contiguous()
     block_counts = block_counts.contiguous()
@@ -54,4 +58,5 @@ def longcat_flash_attn(q, k, v, block_indices, block_counts, sm_scale=None, logi
         raise ValueError(f"K Length ({K_len}) must be divisible by logical_block_size ({BLOCK_N})")
     if block_indices.numel() and (int(block_indices.max()) >= K_len // BLOCK_N or int(block_indices.min()) < 0):
         raise ValueError("Sparse indices out of bounds.")
-    return _core.bsa_forward(q, k, v, block_indices, block_counts, sm_scale, BLOCK_N)
+    o = _core.bsa_forward(q, k, v, block_indices, block_counts, sm_scale, BLOCK_N)
+    return o if o.dtype == out_dtype else o.to(out_dtype)

@@ -18,8 +18,9 @@ from ..hy.bi_sparse_operation_for_KV_cache import generate_prefill_indices as _p
 ENABLE_SPARSE_PROFILING = False
 
 
-def generate_prefill_indices(q_in, k_in, text_len, grid_thw, params, device):
-    return _prefill_indices(q_in, k_in, text_len, grid_thw, params, device, default_ratio=0.25)
+def generate_prefill_indices(q_in, k_in, text_len, grid_thw, params, device, *, k_pool_normalized=None):
+    return _prefill_indices(q_in, k_in, text_len, grid_thw, params, device, default_ratio=0.25,
+                            k_pool_normalized=k_pool_normalized)
 
 
 def run_sparse_attention(q, k, v, text_len, block_idx, latent_hw, sparse_params):
@@ -38,11 +39,13 @@ def run_sparse_attention(q, k, v, text_len, block_idx, latent_hw, sparse_params)
     k_txt = k[:, :, :text_len] if text_len > 0 else None
     v_txt = v[:, :, :text_len] if text_len > 0 else None
 
-    def select(q_pool, k_pool, tl, grid_q, grid_k):
-        return generate_prefill_indices(q_pool, k_pool, tl, grid_k, dict(sparse_params, tile_size=tile), q.device)
+    def select(q_pool, k_pool, tl, grid_q, grid_k, k_pool_normalized=None):
+        return generate_prefill_indices(q_pool, k_pool, tl, grid_k, dict(sparse_params, tile_size=tile), q.device,
+                                        k_pool_normalized=k_pool_normalized)
 
+    # The block mask lists every row's text blocks first (ascending ids).
     o = _pipeline.sparse_attention(q, k_txt, v_txt, k[:, :, text_len:], v[:, :, text_len:], latent_hw, tile,
-                                   select, events, balance=_pipeline.ragged(sparse_params),
+                                   select, events, sorted_lists=True, balance=_pipeline.ragged(sparse_params),
                                    qk_fp8=_pipeline.qk_fp8(sparse_params),
                                    context=_pipeline.context_of(sparse_params, block_idx),
                                    normalize_k_pool=_pipeline.cosine(sparse_params))

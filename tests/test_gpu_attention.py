@@ -186,20 +186,32 @@ def test_out_of_range_ids_are_skipped_and_wrapper_raises(dev):
 
 
 def test_longcat_entry_fp32_inputs_and_strided_indices(dev):
+    """float32 q/k/v through both entry points: the HY entry returns q's dtype (its reference allocates the
+    output with torch.empty_like(q), longcat_kernel.py:198), the MG entry bf16 (its reference casts non-half
+    inputs to bf16 first, matrix-game-3.0 longcat_kernel.py:139-147).  Both compute in bf16; the oracle runs
+    in float64 on the float32 inputs themselves, so the tolerance also covers the bf16 input rounding."""
     print("[gpu] longcat_flash_attn fp32 inputs, non-contiguous indices", flush=True)
     bs, D = 128, 128
-    q, k, v = _inputs(41, 1, 2, 3 * bs, 5 * bs, D)
+    g = torch.Generator().manual_seed(41)
+    q = torch.randn(1, 2, 3 * bs - 30, D, generator=g) / math.sqrt(D) * 2
+    k = torch.randn(1, 2, 5 * bs, D, generator=g)
+    v = torch.randn(1, 2, 5 * bs, D, generator=g)
     rng = np.random.default_rng(4)
     ind, cnt = _random_lists(rng, 1, 2, 3, 5, 4, allow_empty=False)
     wide = np.zeros((1, 2, 3, 8), np.int32)
     wide[..., ::2] = ind
     ind_view = torch.from_numpy(wide).to(dev)[..., ::2]
-    out = mg_longcat_flash_attn(q.float().to(dev), k.float().to(dev), v.float().to(dev), ind_view,
-                                torch.from_numpy(cnt).to(dev))
-    torch.cuda.synchronize()
-    assert out.dtype == torch.bfloat16
-    o_ref, _ = oatt.bsa_forward(_f64(q), _f64(k), _f64(v), ind, cnt, 1.0 / math.sqrt(D), bs)
-    assert np.abs(out.float().cpu().numpy() - o_ref).max() <= TOL
+    o_ref, _ = oatt.bsa_forward(q.double().numpy(), k.double().numpy(), v.double().numpy(), ind, cnt,
+                                1.0 / math.sqrt(D), bs)
+    for name, entry, want in (("hy", longcat_flash_attn, torch.float32),
+                              ("mg", mg_longcat_flash_attn, torch.bfloat16)):
+        out = entry(q.to(dev), k.to(dev), v.to(dev), ind_view, torch.from_numpy(cnt).to(dev))
+        torch.cuda.synchronize()
+        err = np.abs(out.float().cpu().numpy() - o_ref).max()
+        print(f"[gpu]   {name}: dtype {out.dtype}, max abs err vs float64 {err:.3e}", flush=True)
+        assert out.dtype == want
+        assert out.shape == q.shape and out.is_contiguous()
+        assert err <= TOL
 
 
 def test_balanced_order_gives_the_same_bits(dev):

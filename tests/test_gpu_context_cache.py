@@ -74,8 +74,9 @@ def test_cached_cosine_calls_with_the_normalised_key_pool(dev, text):
     wl = _wl()
     params = dict(wl.sparse_params(), tile_size=wl.tile, sim_metric="cosine")
 
-    def select(q_pool, k_pool, tl, grid_q, grid_k):
-        return fast_generate_indices(q_pool, k_pool, tl, grid_q, grid_k, params, dev)
+    def select(q_pool, k_pool, tl, grid_q, grid_k, k_pool_normalized=None):
+        return fast_generate_indices(q_pool, k_pool, tl, grid_q, grid_k, params, dev,
+                                     k_pool_normalized=k_pool_normalized)
 
     def call(q, k, v, kt, vt, context, norm):
         return _pipeline.sparse_attention(q, kt, vt, k, v, wl.latent_hw, wl.tile, select, context=context,

@@ -102,6 +102,13 @@ def test_direct_calls_check_extents(dev):
     kp = torch.zeros((1, 2, 8, 128), dtype=torch.bfloat16, device=dev)
     ind, cnt = _lists(dev, 2, 4, 8, 5)
     scale = 1.0 / math.sqrt(128)
+    txt = torch.zeros((1, 2, 128, 128), dtype=torch.bfloat16, device=dev)
+    txt_long = torch.zeros((1, 2, 256, 128), dtype=torch.bfloat16, device=dev)
+    q8 = torch.zeros((1, 2, 512, 128), dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    k8 = torch.zeros((1, 2, 1024, 128), dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    qs_long = torch.ones((1, 2, 5), dtype=torch.float32, device=dev)
+    ks = torch.ones((1, 2, 8), dtype=torch.float32, device=dev)
+    vt = torch.zeros((1, 2, 1024, 128), dtype=torch.bfloat16, device=dev)
     cases = [
         ("src must", lambda: torch.ops.li.pool(short_k, kp, 0, gk)),
         ("mean must", lambda: torch.ops.li.pool(k, kp[:, :, :7], 0, gk)),
@@ -124,6 +131,13 @@ def test_direct_calls_check_extents(dev):
                                                       False, True, False)),
         ("v must", lambda: torch.ops.li.attn_dense(q, k, v[:, :, :-128], None, None, 0, scale, torch.empty_like(q),
                                               False, True)),
+        # Over-long contiguous tensors the kernels index at a per-head pitch: exact extents only.
+        ("k_txt must", lambda: torch.ops.li.bsa_fwd_gather(q, k, v, txt_long, txt, 1, gq, gk, ind, cnt, scale,
+                                                      torch.empty_like(q), False, True, False)),
+        ("v_txt must", lambda: torch.ops.li.attn_dense(q, k, v, txt, txt_long, 100, scale, torch.empty_like(q),
+                                                  False, True)),
+        ("q_scale must", lambda: torch.ops.li.bsa_fwd_fp8(q8, qs_long, k8, ks, vt, ind, cnt, scale, 128,
+                                                     torch.empty_like(vt[:, :, :512]), False, True, False)),
     ]
     for what, call in cases:
         with pytest.raises(RuntimeError, match=what):

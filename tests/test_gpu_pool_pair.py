@@ -143,9 +143,8 @@ def test_mask_through_normalized_pool(kernel):
               force_neighbors=True, return_scores=True)
     raw = _core.block_mask(qp, kp, **kw)
     kp2 = pool_buf().copy_(kp)
-    _core.attach_normalized(kp2, kn)
-    via = _core.block_mask(qp, kp2, **kw)
-    dot = _core.block_mask(qp, kp2, **dict(kw, metric="dot"))  # other metrics ignore the normalised copy
+    via = _core.block_mask(qp, kp2, k_pool_normalized=kn, **kw)
+    dot = _core.block_mask(qp, kp2, k_pool_normalized=kn, **dict(kw, metric="dot"))  # other metrics ignore it
     dot_raw = _core.block_mask(qp, kp, **dict(kw, metric="dot"))
     torch.cuda.synchronize()
     for a, b in zip(raw, via):

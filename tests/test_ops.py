@@ -77,3 +77,40 @@ def test_ops_trace_under_fake_tensor_mode():
         ind, cnt, _ = torch.ops.li.block_mask.default(qp.to("meta"), kp.to("meta"), 0, 1, 0.5, 7, 0, False, False,
                                                       True, 2, 2, 0, 9, None, False)
         assert ind.shape == (1, 2, 8, 9)
+
+
+def test_fake_rejects_over_long_pitch_indexed_tensors():
+    """Tensors the kernels index at a per-head pitch implied by the geometry (contiguous padded text K/V, e4m3
+    tiles and scales) must have exactly that extent: a longer contiguous tensor would make every head after the
+    first read another head's rows.  The operators raise for it before tracing (meta tensors, no GPU)."""
+    q = _t((1, 6240, 16, 128)).permute(0, 2, 1, 3)
+    k = _t((1, 18720, 16, 128)).permute(0, 2, 1, 3)
+    ind, cnt = _t((1, 16, 56, 53), torch.int32), _t((1, 16, 56), torch.int32)
+    out = torch.empty_like(q)
+    geo_q, geo_k = [4, 30, 52, 2, 8, 8, 4, 7], [12, 30, 52, 2, 8, 8, 4, 7]
+    txt = _t((1, 16, 256, 128))
+    ops.bsa_fwd_gather(q, k, k, txt, txt, 2, geo_q, geo_k, ind, cnt, 0.088, out, False, True, False)
+    for bad in (_t((1, 16, 384, 128)), _t((1, 16, 128, 128))):
+        with pytest.raises(RuntimeError, match="k_txt must be"):
+            ops.bsa_fwd_gather(q, k, k, bad, txt, 2, geo_q, geo_k, ind, cnt, 0.088, out, False, True, False)
+        with pytest.raises(RuntimeError, match="v_txt must be"):
+            ops.bsa_fwd_gather(q, k, k, txt, bad, 2, geo_q, geo_k, ind, cnt, 0.088, out, False, True, False)
+    with pytest.raises(RuntimeError, match="k_txt must be"):
+        ops.attn_dense(q, k, k, _t((1, 16, 384, 128)), txt, 200, 0.088, out, False, True)
+    q8, k8 = _t((1, 16, 7168, 128), torch.float8_e4m3fn), _t((1, 16, 21504, 128), torch.float8_e4m3fn)
+    qs, ks, v = _t((1, 16, 56), torch.float32), _t((1, 16, 168), torch.float32), _t((1, 16, 21504, 128))
+    o = _t((1, 16, 7168, 128))
+    ops.bsa_fwd_fp8(q8, qs, k8, ks, v, ind, cnt, 0.088, 128, o, False, True, False)
+    with pytest.raises(RuntimeError, match="q_scale must be"):
+        ops.bsa_fwd_fp8(q8, _t((1, 16, 57), torch.float32), k8, ks, v, ind, cnt, 0.088, 128, o, False, True, False)
+    with pytest.raises(RuntimeError, match="k_scale must be"):
+        ops.bsa_fwd_fp8(q8, qs, k8, _t((1, 16, 170), torch.float32), v, ind, cnt, 0.088, 128, o, False, True, False)
+    # token-order e4m3: V and O in token order, tiles and scales with two text blocks
+    k8t, kst = _t((1, 16, 170 * 128, 128), torch.float8_e4m3fn), _t((1, 16, 170), torch.float32)
+    ops.bsa_fwd_fp8_gather(q8, qs, k8t, kst, k, txt, 2, geo_q, geo_k, ind, cnt, 0.088, out, False, False, False)
+    for args, what in (((_t((1, 16, 7296, 128), torch.float8_e4m3fn), qs, k8t, kst), "q8 must be"),
+                       ((q8, qs, _t((1, 16, 171 * 128, 128), torch.float8_e4m3fn), kst), "k8 must be"),
+                       ((q8, _t((1, 16, 60), torch.float32), k8t, kst), "q_scale must be"),
+                       ((q8, qs, k8t, _t((1, 16, 171), torch.float32)), "k_scale must be")):
+        with pytest.raises(RuntimeError, match=what):
+            ops.bsa_fwd_fp8_gather(*args, k, txt, 2, geo_q, geo_k, ind, cnt, 0.088, out, False, False, False)
