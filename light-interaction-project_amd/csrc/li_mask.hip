@@ -10,16 +10,19 @@
 // 1. score[j] for every key block j, with the reference's rounding points:
 //    cosine  xn = E(x / max(E(sqrt(sum x^2)), E(1e-12))), sim = E(sum qn*kn);
 //    scaled  sim = E(f32(E(sum q*k)) * scale);  dot  sim = E(sum q*k)
-//    (E = round to the element type).  Every fp32 sum over d runs sequentially
-//    from +0.0; element products are exact in fp32.
+//    (E = round to the element type).  Element products are exact in fp32.
+//    A dot product over d takes eight fp32 partial sums, partial i over
+//    d = i, i+8, ... sequentially from +0.0, combined as
+//    ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7)) (eight short chains instead of one
+//    of D dependent multiply-adds); a sum of squares runs sequentially.
 // 2. forced blocks (recent slabs, diagonal, sink, 3D neighbours) are kept
 //    unconditionally -- the reference's +1e6 bias has the same effect;
 // 3. the budget k follows the reference's integer arithmetic (int() truncation
 //    of a double product) and the remaining k - n_forced blocks are the
 //    largest non-forced scores, ties to the lower index: every key block gets
 //    the unique 32-bit key (order-preserving score bits << 16 | 0xFFFF - j;
-//    0 marks a forced block) and a bitwise search of at most 32 steps finds
-//    the exact (k - n_forced)-th largest key;
+//    0 marks a forced block) and a search two bits at a time finds a
+//    threshold with exactly k - n_forced non-forced keys at or above it;
 // 4. the selected blocks are written in ascending order by a ballot/prefix
 //    compaction over j, which replaces the reference's topk + sort.
 //
@@ -85,6 +88,13 @@ __device__ __forceinline__ float norm_den(const float* x) {
 
 __device__ __forceinline__ int wave_count(bool pred) { return __popcll(__ballot(pred)); }
 
+// The dot product's combination of its eight partial sums.
+__device__ __forceinline__ float sum8(const float* s) {
+  return ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+}
+
+#define LI_SEL_INLINE __attribute__((always_inline))
+
 // Steps 3 and 4 for query row qb of (b, h) = bh, run by one wave: key_at(r)
 // is the key of block 64 r + lane (0 for forced blocks and past nk), nchunk =
 // ceil(nk / 64), nf the number of forced blocks.
@@ -116,31 +126,47 @@ __device__ __forceinline__ void select_row(const MaskArgs& a, KeyAt&& key_at, in
   const int kk = __builtin_amdgcn_readfirstlane(k - nf);  // non-forced blocks to keep
   const int nfree = nk - nf;
 
-  // Threshold thr with exactly kk non-forced keys >= thr: the kk-th largest
-  // key, found bit by bit from the top (forced keys are 0 and never reach a
-  // candidate, which is always >= 1 here).  The search stops as soon as a
-  // candidate has exactly kk keys at or above it -- the same set as the
-  // kk-th largest key selects -- which for distinct scores happens within the
-  // 16 score bits.
-  // Index bits 15 .. L-1 of the low half are 1 in every key (0xFFFF - j with
-  // j < nk <= 2^L), so those steps keep their bit without counting.
+  // Threshold thr with exactly kk non-forced keys >= thr, found from the top
+  // two bits per step: with the bits above settled in `prefix`, the three
+  // candidates prefix|11, prefix|10 and prefix|01 are counted together (their
+  // ballots are independent), and the largest one with at least kk keys at
+  // or above it is kept -- what two single-bit steps would keep.  Forced keys
+  // are 0 and never reach a candidate, which is always >= 1 here.  The search
+  // stops as soon as a kept candidate has exactly kk keys at or above it, the
+  // same set as the kk-th largest key selects; for distinct scores that
+  // happens within the 16 score bits.  Index bits 15 .. L-1 of the low half
+  // are 1 in every key (0xFFFF - j with j < nk <= 2^L): they are set in the
+  // prefix from the start (no key's count changes) and not searched.
   uint32_t thr = 1u;
   if (kk > 0 && kk < nfree) {
     const int L = nk > 1 ? 32 - __builtin_clz((uint32_t)(nk - 1)) : 0;
-    uint32_t prefix = 0;
-    for (int bit = 31; bit >= 0; --bit) {
-      if (bit < 16 && bit >= L) {
-        prefix |= 1u << bit;
-        continue;
-      }
-      const uint32_t cand = prefix | (1u << bit);
-      int c = 0;
+    // The searched bit below b, or -1.
+    auto below = [&](int b) LI_SEL_INLINE { return b - 1 >= 16 || b - 1 < L ? b - 1 : L - 1; };
+    uint32_t prefix = 0xFFFFu & ~((1u << L) - 1u);
+    int b1 = 31;
+    while (b1 >= 0) {
+      const int b0 = below(b1);
+      const uint32_t m1 = 1u << b1, m0 = b0 >= 0 ? 1u << b0 : 0u;
+      const uint32_t c3 = prefix | m1 | m0, c2 = prefix | m1, c1 = prefix | m0;
+      int n3 = 0, n2 = 0, n1 = 0;
 #pragma unroll KUNROLL
-      for (int r = 0; r < nchunk; ++r) c += wave_count(key_at(r) >= cand);
-      if (c >= kk) {
-        prefix = cand;
-        if (c == kk) break;
+      for (int r = 0; r < nchunk; ++r) {
+        const uint32_t key = key_at(r);
+        n3 += wave_count(key >= c3);
+        n2 += wave_count(key >= c2);
+        n1 += wave_count(key >= c1);
       }
+      if (n3 >= kk) {
+        prefix = c3;
+        if (n3 == kk) break;
+      } else if (n2 >= kk) {
+        prefix = c2;
+        if (n2 == kk) break;
+      } else if (m0 != 0u && n1 >= kk) {
+        prefix = c1;
+        if (n1 == kk) break;
+      }
+      b1 = b0 >= 0 ? below(b0) : -1;
     }
     thr = prefix;
   }
@@ -250,15 +276,16 @@ __global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a, int waves) 
     if (j < nk) {
       float x[D];
       load_row<E, D>(kbase + (int64_t)j * a.ks[2], a.ks[3], vec, x);
-      float dot = 0.0f;
+      float ps[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
       if (cosine && !p.k_normalized) {
         const float den = norm_den<E, D>(x);
 #pragma unroll
-        for (int d = 0; d < D; ++d) dot = dot + qv[d] * E::to_f32(E::from_f32(x[d] / den));
+        for (int d = 0; d < D; ++d) ps[d & 7] = ps[d & 7] + qv[d] * E::to_f32(E::from_f32(x[d] / den));
       } else {
 #pragma unroll
-        for (int d = 0; d < D; ++d) dot = dot + qv[d] * x[d];
+        for (int d = 0; d < D; ++d) ps[d & 7] = ps[d & 7] + qv[d] * x[d];
       }
+      const float dot = sum8(ps);
       keys[j] = finish_key<E>(p, g, srow, j, dot, f);
     }
     nf += wave_count(f);
@@ -280,7 +307,7 @@ __global__ __launch_bounds__(256) void block_mask_kernel(MaskArgs a, int waves) 
 // blocks hit distinct banks.  For cosine, thread t computes the normaliser of
 // block t of the tile and the whole workgroup then divides the tile in place
 // before the dot products.  Per (row, block) the arithmetic is the generic
-// path's: the same sequential fp32 sum over d of the same operands.  The next
+// path's: the same fp32 sums over d of the same operands.  The next
 // tile's loads are in flight while the current one is scored, and the first
 // wave of each row then selects with the row's keys in registers
 // (nk <= 64 KS).
@@ -384,14 +411,15 @@ __global__ __launch_bounds__(512) void block_mask_tiled_kernel(MaskArgs a) {
       // Tile rows past nt hold stale data; their sums are computed and
       // dropped, so the LDS reads carry no branch and can be issued ahead.
       const int jl = lane + 64 * half;
-      float dot = 0.0f;
+      float ps[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
         const u32x4 w = *reinterpret_cast<const u32x4*>(ktile + jl * RS + 16 * c);
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          dot = dot + qr[8 * c + e] * E::to_f32(uint16_t((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu));
+          ps[e] = ps[e] + qr[8 * c + e] * E::to_f32(uint16_t((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu));
       }
+      const float dot = sum8(ps);
       bool f = false;
       if (jl < nt) keys[j0 + jl] = finish_key<E>(p, g, srow, j0 + jl, dot, f);
       nf += wave_count(f);

@@ -19,8 +19,11 @@ Rounding model (the reference computes these with bf16 torch ops):
   (ar_sparse_operation.py:254, bi_sparse_operation_for_KV_cache.py:258-260);
 * dot: ``sim = bf16(sum_d q*k)`` (ar_sparse_operation.py:256).
 
-Every fp32 sum over d is sequential from +0.0 in increasing d (bf16*bf16
-products are exact in fp32, so fused and unfused multiply-add agree).
+Sums over d are in fp32 with bf16*bf16 products exact in fp32 (so fused and
+unfused multiply-add agree).  A dot product takes eight partial sums, partial
+i over d = i, i+8, i+16, ... sequentially from +0.0, combined as
+((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7)); a sum of squares (the normaliser) is
+sequential from +0.0 in increasing d.
 
 float16 pools (``fmt="f16"``) follow the same model with every bf16 rounding
 replaced by an IEEE half rounding (the reference's ops then run in float16);
@@ -69,13 +72,18 @@ def f32_to_f16(x):
 FORMATS = {"bf16": (bf16_to_f32, f32_to_bf16), "f16": (f16_to_f32, f32_to_f16)}
 
 
-def _seq_dot(a, b):
-    """Sequential fp32 dot over the last axis: a (..., M, D), b (..., N, D) -> (..., M, N)."""
+def _dot8(a, b):
+    """fp32 dot over the last axis: a (..., M, D), b (..., N, D) -> (..., M, N), D a multiple of 8.
+
+    Eight partial sums, partial i over d = i, i+8, ... sequentially from +0.0, then
+    ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7)): the order both mask kernels use.
+    """
     D = a.shape[-1]
-    acc = np.zeros(a.shape[:-1] + (b.shape[-2],), dtype=np.float32)
+    assert D % 8 == 0, "the dot order is defined for D a multiple of 8"
+    s = [np.zeros(a.shape[:-1] + (b.shape[-2],), dtype=np.float32) for _ in range(8)]
     for d in range(D):
-        acc = acc + a[..., :, None, d] * b[..., None, :, d]
-    return acc
+        s[d % 8] = s[d % 8] + a[..., :, None, d] * b[..., None, :, d]
+    return ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]))
 
 
 def _normalize_bits(x_bits, fmt="bf16"):
@@ -98,8 +106,8 @@ def similarity(q_pool_bits, k_pool_bits, metric, fmt="bf16"):
     to32, from32 = FORMATS[fmt]
     if metric == "cosine":
         qn, kn = _normalize_bits(q_pool_bits, fmt), _normalize_bits(k_pool_bits, fmt)
-        return from32(_seq_dot(to32(qn), to32(kn)))
-    dot = from32(_seq_dot(to32(q_pool_bits), to32(k_pool_bits)))
+        return from32(_dot8(to32(qn), to32(kn)))
+    dot = from32(_dot8(to32(q_pool_bits), to32(k_pool_bits)))
     if metric == "scaled_dot_product":
         d = q_pool_bits.shape[-1]
         scale = np.float32(1.0 / math.sqrt(d))
