@@ -703,6 +703,22 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     }
     lrow += ls;
   };
+  // The softmax of a tile's first block (mrow = -inf, l = 0, O = 0), which
+  // always takes the slow path above: the block max first, then one set of
+  // exponentials; O and l need no rescale.  The same values as softmax().
+  auto softmax_first = [&]() LI_INLINE {
+    float mx = sacc[0][0];
+#pragma unroll
+    for (int kt = 0; kt < C::NKT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, sacc[kt][r]);
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    mx = __builtin_fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * qk_scale;
+    const float mnew = __builtin_fmaxf(mrow, mx);
+    const float msafe = mnew == -__builtin_inff() ? 0.0f : mnew;
+    mrow = mnew;
+    lrow = exps(msafe);
+  };
   // O^T += V^T P^T.
   auto pv_update = [&](const char* vd) LI_INLINE {
 #pragma unroll
@@ -1102,7 +1118,13 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       scores(ks1);
       if (!load) barrier();
       if constexpr (F8) qk_scale = qk_base * ksc[safe(id_c)];
-      x_phase(id_c, [] {});
+      if (valid(id_c)) {
+        mask_tail(id_c);
+        softmax_first();
+      } else {
+#pragma unroll
+        for (int st = 0; st < C::PST; ++st) ppk[st] = u32x4{0u, 0u, 0u, 0u};
+      }
       if (load) wait_loads();
       if (!load) {
         for (int i = 0; i < count; i += 2) {
