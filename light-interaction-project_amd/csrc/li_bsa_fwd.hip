@@ -1203,8 +1203,13 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
     }
   }
 
-  // Merge the two key halves (waves kh = 0 and kh = 1 of the same qq).
-  lrow += __shfl_xor(lrow, 32);
+  // Merge the two key halves (waves kh = 0 and kh = 1 of the same qq).  The
+  // exchanged O of a wave is stored as 16-byte runs: element (dt, 4 i4 + j)
+  // of lane l at ((dt * 4 + i4) * 64 + l) * 4 + j.
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(lrow), __float_as_uint(lrow), false, false);
+    lrow = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
   char* xo_st = F8 ? (qq < C::NQW / 2 || C::NQW == 1 ? vs0 : vs1) : (qq < C::NQW / 2 || C::NQW == 1 ? ks0 : ks1);
   float* xo = reinterpret_cast<float*>(xo_st) + (qq % (C::NQW > 1 ? C::NQW / 2 : 1)) * (C::NDT * 16 * 64);
   float* xm = reinterpret_cast<float*>(F8 ? ks0 : vs0) + qq * (2 * 64);
@@ -1212,7 +1217,9 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
 #pragma unroll
     for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) xo[(dt * 16 + r) * 64 + lane] = o[dt][r];
+      for (int i4 = 0; i4 < 4; ++i4)
+        *reinterpret_cast<f32x4*>(xo + ((dt * 4 + i4) * 64 + lane) * 4) =
+            f32x4{o[dt][4 * i4], o[dt][4 * i4 + 1], o[dt][4 * i4 + 2], o[dt][4 * i4 + 3]};
     xm[lane] = mrow;
     xm[64 + lane] = lrow;
   }
@@ -1232,12 +1239,10 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) {
+          const f32x4 o1 = *reinterpret_cast<const f32x4*>(xo + ((dt * 4 + i4) * 64 + lane) * 4);
           f32x4 val;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int rr = 4 * i4 + j;
-            val[j] = o[dt][rr] * a0 + xo[(dt * 16 + rr) * 64 + lane] * a1;
-          }
+          for (int j = 0; j < 4; ++j) val[j] = o[dt][4 * i4 + j] * a0 + o1[j] * a1;
           *reinterpret_cast<f32x4*>(prow + 32 * dt + 8 * i4 + 4 * hl) = val;
         }
       if (hl == 0) {
@@ -1251,12 +1256,10 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
         for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
           for (int i4 = 0; i4 < 4; ++i4) {
+            const f32x4 o1 = *reinterpret_cast<const f32x4*>(xo + ((dt * 4 + i4) * 64 + lane) * 4);
             float val[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int rr = 4 * i4 + j;
-              val[j] = (o[dt][rr] * a0 + xo[(dt * 16 + rr) * 64 + lane] * a1) * inv;
-            }
+            for (int j = 0; j < 4; ++j) val[j] = (o[dt][4 * i4 + j] * a0 + o1[j] * a1) * inv;
             const u32x2 pk = {cvt_pk<E>(val[0], val[1]), cvt_pk<E>(val[2], val[3])};
             *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i4 + 4 * hl) = pk;
           }
