@@ -73,6 +73,10 @@ WORKLOADS = {
     "hy_fp8": Workload("hy_fp8", 16, 128, (30, 52), 4, 12, (2, 8, 8), 0.3, "scaled_dot_product", qk_fp8=True,
                        note="HY shape with Q, K as e4m3 codes and per-128-token-block fp32 scales (amax/448), "
                             "V bf16: e4m3 MFMA for Q K^T, bf16 for P V; the same selection as hy"),
+    "hy_long_fp8": Workload("hy_long_fp8", 16, 128, (30, 52), 4, 64, (2, 8, 8), 0.1, "scaled_dot_product",
+                            ragged=(8, 200), qk_fp8=True,
+                            note="HY long rollout (as hy_long) with Q, K as e4m3 codes and per-128-token-block "
+                                 "scales, V bf16; the same selection as hy_long"),
 }
 
 
