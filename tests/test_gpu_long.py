@@ -89,3 +89,40 @@ def test_long_rollout_orders_and_paths_same_bits(dev, long_case):
     d = (out_nat.float() - out_whole.float()).abs().max().item()
     print(f"[gpu]   natural order (tail split) vs whole tiles: {d:.3e}", flush=True)
     assert d <= 1e-2
+
+
+def test_long_rollout_e4m3_call_vs_oracle(dev, long_case):
+    """The e4m3 call (qk_fp8) at the long-rollout shape: sampled tiles (longest and shortest rows included) against
+    the oracle pipeline on the quantized Q and K, and the fused longest-first kernel bit-equal to the tiled e4m3
+    sequence on the same lists."""
+    wl, q, k, v, g = long_case
+    params = WORKLOADS["hy_long_fp8"].sparse_params(g.nq_blk)
+    assert params["qk_fp8"] and params["row_budget"] == wl.sparse_params(g.nq_blk)["row_budget"]
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    e = torch.empty((1, wl.heads, 0, wl.head_dim), dtype=torch.bfloat16, device=dev)
+    print("[gpu] run_sparse_attention hy_long_fp8 (fused e4m3, longest tiles first)", flush=True)
+    out = run_sparse_attention(qd, e, e, kd, vd, 1, wl.latent_hw, params)
+
+    def select(q_pool, k_pool, text_len, grid_q, grid_k):
+        return fast_generate_indices(q_pool, k_pool, text_len, grid_q, grid_k, params, dev)
+
+    out_til = _pipeline.sparse_attention(qd, None, None, kd, vd, wl.latent_hw, wl.tile, select, balance=True,
+                                         qk_fp8=True, fused=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out_til.view(torch.int16))
+    budgets = np.asarray(params["row_budget"])
+    longest, shortest = int(np.argmax(budgets)), int(np.argmin(budgets))
+    rng = np.random.default_rng(5)
+    tiles = [(0, 1, longest), (0, wl.heads - 2, shortest)]
+    tiles += [(0, int(h), int(m)) for h, m in zip(rng.integers(0, wl.heads, 8), rng.integers(0, g.nq_blk, 8))]
+    print(f"[gpu]   oracle (quantized Q, K) on {len(tiles)} tiles", flush=True)
+    ref = oracle_pipeline(q, k, v, wl.latent_hw, params, heads=tiles)
+    got = out.float().cpu().numpy()
+    bs, perm = ref["geo"]["BS"], ref["perm"]
+    err = 0.0
+    for b, h, m in tiles:
+        rows = perm[m * bs:(m + 1) * bs]
+        rows = rows[rows >= 0]
+        err = max(err, np.abs(got[b, h, rows] - ref["out"][b, h, rows]).max())
+    print(f"[gpu]   max abs err over {len(tiles)} sampled tiles {err:.3e}", flush=True)
+    assert err <= TOL
