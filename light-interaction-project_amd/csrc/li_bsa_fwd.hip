@@ -1107,6 +1107,14 @@ __global__ __launch_bounds__(4 * BS) void bsa_fwd_dma_kernel(BsaArgs a) {
       };
       if (i + 1 < count) x_phase(id_x, next_sources);
       if (load) wait_loads();
+      // The scalar loads of this phase (the next block id, and for F8 a K
+      // scale) complete here, before the next M phase: one still in flight
+      // there would make its first operand wait cover all LA MFMAs' LDS reads
+      // (lgkmcnt counts both, and scalar loads return out of order).
+      if constexpr (F8)
+        __asm__ volatile("" ::"s"(id_n3), "s"(sk_nn));
+      else
+        __asm__ volatile("" ::"s"(id_n3));
     };
     auto run = [&](bool load) LI_INLINE {
       if (load) {
