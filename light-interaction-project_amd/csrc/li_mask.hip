@@ -202,7 +202,17 @@ template <typename E, int D>
 __device__ __forceinline__ void load_query(const MaskArgs& a, int b, int h, int qb, bool cosine, float* qv,
                                            int lane) {
   const uint16_t* qrow = a.qp + b * a.qs[0] + h * a.qs[1] + (int64_t)qb * a.qs[2];
-  for (int d = lane; d < D; d += 64) qv[d] = E::to_f32(qrow[(int64_t)d * a.qs[3]]);
+  // All of the lane's loads are issued before the first is used.
+  constexpr int PER = (D + 63) / 64;
+  uint16_t x[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int d = lane + 64 * i;
+    x[i] = d < D ? qrow[(int64_t)d * a.qs[3]] : uint16_t(0);
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i)
+    if (lane + 64 * i < D) qv[lane + 64 * i] = E::to_f32(x[i]);
   __builtin_amdgcn_wave_barrier();
   if (cosine) {
     float ss = 0.0f;
@@ -343,12 +353,16 @@ __global__ __launch_bounds__(512) void block_mask_tiled_kernel(MaskArgs a) {
   // Chunk i of this thread: tile row tid / CH + i * (NTHR / CH), column tid % CH.
   const int r0 = tid / CH, cc = tid % CH;
   u32x4 pf[PF];
+  // The chunks of tile rows past nt repeat the last row: every load is
+  // issued unconditionally, so they all go out together, and only rows below
+  // nt are stored.
   auto fetch = [&](int j0) LI_MASK_INLINE {
     const int nt = nk - j0 < NT ? nk - j0 : NT;
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
       const int r = r0 + i * (NTHR / CH);
-      if (r < nt) pf[i] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)(j0 + r) * a.ks[2] + 8 * cc);
+      const int rr = r < nt ? r : nt - 1;
+      pf[i] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)(j0 + rr) * a.ks[2] + 8 * cc);
     }
   };
   fetch(0);
