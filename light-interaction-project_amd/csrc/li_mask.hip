@@ -355,7 +355,7 @@ __global__ __launch_bounds__(512) void block_mask_tiled_kernel(MaskArgs a) {
   u32x4 pf[PF];
   // The chunks of tile rows past nt repeat the last row: every load is
   // issued unconditionally, so they all go out together, and only rows below
-  // nt are stored.
+  // nt are stored.  A tile is fetched only at j0 < nk, so nt >= 1.
   auto fetch = [&](int j0) LI_MASK_INLINE {
     const int nt = nk - j0 < NT ? nk - j0 : NT;
 #pragma unroll
@@ -365,7 +365,7 @@ __global__ __launch_bounds__(512) void block_mask_tiled_kernel(MaskArgs a) {
       pf[i] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)(j0 + rr) * a.ks[2] + 8 * cc);
     }
   };
-  fetch(0);
+  if (nk > 0) fetch(0);  // no key blocks: nothing to read
   __syncthreads();  // the query rows are visible to both waves of their row
   // The query row in registers for the dot products (wave-uniform values;
   // stale on dead waves, never used there).

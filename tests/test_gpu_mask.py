@@ -1,4 +1,5 @@
 """GPU parity: block-mask builder vs the oracle (bit-exact scores, indices, counts) and the golden fixtures."""
+import ctypes
 import math
 import os
 
@@ -106,6 +107,38 @@ def test_five_d_input_and_ties(dev):
         free = [j for j in range(8) if not forced[r, j]]
         want = sorted(list(np.nonzero(forced[r])[0]) + free[:max(0, 7 - int(forced[r].sum()))])
         assert ind[0, 0, r].tolist() == want
+
+
+@pytest.mark.parametrize("metric", ["cosine", "dot"])
+def test_no_key_blocks(dev, metric):
+    """A key grid with no blocks (nk = 0), through the C ABI with a valid key-pool pointer (torch gives a
+    zero-row tensor a null pointer, which the entry point rejects): the shared-pool kernel reads no pool row and
+    every query row keeps only its text blocks, as the oracle's selection does; the rest of the row is zero."""
+    print(f"[gpu] mask nk=0 metric={metric}", flush=True)
+    D, nq, nh, nw, ntxt, kmax = 128, 6, 2, 3, 2, 3
+    gen = torch.Generator().manual_seed(7)
+    qp = torch.randn(1, 2, nq, D, generator=gen).to(torch.bfloat16)
+    qd = qp.to(dev)
+    kbuf = torch.randn(1, 2, 4, D, generator=gen).to(torch.bfloat16).to(dev)
+    geo = {"nq_blk": nq, "nk_blk": 0, "nh": nh, "nw": nw}
+    params = {"tile_size": (2, 8, 8), "topk_ratio": 0.3, "force_diag": True, "force_sink": True}
+    forced, kk = oracle_forced(geo, params, "decode")
+    oind, ocnt, _, _ = omask.build_indices(bits(qp), np.zeros((1, 2, 0, D), np.uint16), metric=metric,
+                                           forced=forced, k=kk, num_txt_blk=ntxt)
+    ind = torch.full((1, 2, nq, kmax), -7, dtype=torch.int32, device=dev)
+    cnt = torch.full((1, 2, nq), -7, dtype=torch.int32, device=dev)
+    code = _core.METRICS.get(metric, _lib.LI_METRIC_DOT)
+    p = _lib.MaskParams(metric=code, budget_mode=_lib.LI_BUDGET_HISTORY, topk_ratio=0.3, min_budget=7, force_diag=1, force_sink=1, nq=nq, nk=0, nh=nh, nw=nw, num_txt_blk=ntxt,
+                        kmax=kmax)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    st = _lib.lib.li_block_mask(_lib.LI_DTYPE_BF16, 1, 2, D, qd.data_ptr(), _lib.i64_array(qd.stride()),
+                                kbuf.data_ptr(), _lib.i64_array(kbuf.stride()), ctypes.byref(p), ind.data_ptr(),
+                                cnt.data_ptr(), None, ctypes.c_void_p(stream))
+    torch.cuda.synchronize()
+    assert st == _lib.LI_OK
+    assert np.array_equal(cnt.cpu().numpy(), ocnt)
+    assert np.array_equal(ind[..., :ntxt].cpu().numpy(), oind)
+    assert (ind[..., ntxt:] == 0).all()
 
 
 @pytest.mark.parametrize("metric", ["cosine", "scaled_dot_product", "dot"])
