@@ -128,8 +128,8 @@ def test_no_key_blocks(dev, metric):
     ind = torch.full((1, 2, nq, kmax), -7, dtype=torch.int32, device=dev)
     cnt = torch.full((1, 2, nq), -7, dtype=torch.int32, device=dev)
     code = _core.METRICS.get(metric, _lib.LI_METRIC_DOT)
-    p = _lib.MaskParams(metric=code, budget_mode=_lib.LI_BUDGET_HISTORY, topk_ratio=0.3, min_budget=7, force_diag=1, force_sink=1, nq=nq, nk=0, nh=nh, nw=nw, num_txt_blk=ntxt,
-                        kmax=kmax)
+    p = _lib.MaskParams(metric=code, budget_mode=_lib.LI_BUDGET_HISTORY, topk_ratio=0.3, min_budget=7,
+                        force_diag=1, force_sink=1, nq=nq, nk=0, nh=nh, nw=nw, num_txt_blk=ntxt, kmax=kmax)
     stream = torch.cuda.current_stream(dev).cuda_stream
     st = _lib.lib.li_block_mask(_lib.LI_DTYPE_BF16, 1, 2, D, qd.data_ptr(), _lib.i64_array(qd.stride()),
                                 kbuf.data_ptr(), _lib.i64_array(kbuf.stride()), ctypes.byref(p), ind.data_ptr(),
