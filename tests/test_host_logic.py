@@ -68,3 +68,16 @@ def test_forced_blocks_and_tie_free_fraction_match_oracle():
         want = np.mean([omask.tie_free(b[i], forced, k) for i in range(2)])
         got = _core.tie_free_fraction(bits, counts, forced)
         assert abs(got - want) < 1e-12 and 0.0 < got < 1.0
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus above 1 exits with status 2 and says so, before touching any device."""
+    import os
+    import subprocess
+    import sys
+
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(repo, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU only" in r.stderr
